@@ -1,0 +1,198 @@
+/*
+ * dspark.h — C ABI of the MI355X (gfx950) speculative-verify kernels.
+ *
+ * Three kernel families sit behind this boundary:
+ *   1. the small-M affine-quantized matmul (4/8-bit, group 64, M = 1..16 verify rows);
+ *   2. multi-row causal GQA verify attention over a strided KV cache (split-KV + combine);
+ *   3. MoE top-k routing plus the grouped expert qmm (gather_qmm / SwitchGLU).
+ * plus the small elementwise kernels a dense verify forward needs around them.
+ *
+ * Conventions (every entry point):
+ *   - Plain pointers and sizes only; device pointers come from the caller (torch tensors).
+ *     No entry point allocates, frees or synchronizes. Work is enqueued on `stream`
+ *     (a hipStream_t; NULL = the legacy default stream).
+ *   - Returns DSPARK_OK (0) or a negative dspark_status; the message for the last failure
+ *     on the calling host thread is in dspark_last_error(). Nothing aborts.
+ *   - bf16 tensors are passed as `const void*` / `void*` holding IEEE bfloat16 (uint16 bits).
+ *   - Strides are in elements.
+ *
+ * Each declaration cites the reference interface it replaces (file:line in ARahim3/mlx-dspark
+ * v0.20.4, src/mlx_dspark/ unless noted).
+ */
+#ifndef DSPARK_H_
+#define DSPARK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* dspark_stream; /* hipStream_t */
+
+enum dspark_status {
+  DSPARK_OK = 0,
+  DSPARK_ERR_ARG = -1,       /* null pointer or bad enum value */
+  DSPARK_ERR_SHAPE = -2,     /* unsupported shape (K % 64, head_dim, M range, ...) */
+  DSPARK_ERR_ALIGN = -3,     /* pointer / stride alignment the kernel's vector loads need */
+  DSPARK_ERR_WORKSPACE = -4, /* workspace missing or too small */
+  DSPARK_ERR_LAUNCH = -5,    /* hipLaunchKernel / hipGetLastError failure */
+  DSPARK_ERR_UNSUPPORTED = -6 /* bits / group size / dtype the kernels do not implement */
+};
+
+/* Library version string and the gfx target the code objects were built for. */
+const char* dspark_version(void);
+/* Message of the last failed call on this host thread ("" if none). */
+const char* dspark_last_error(void);
+
+/* ------------------------------------------------------------------ small-M quantized matmul */
+
+/*
+ * y[m, n] = sum_g ( scale[n,g] * sum_{j in g} q[n,j] * x[m,j]  +  bias[n,g] * sum_{j in g} x[m,j] )
+ * fp32 accumulation, bf16 output, for M = 1..16 rows (M > 16 is served in 16-row tiles).
+ *
+ * x       bf16 [M, K], row stride ldx (ldx % 8 == 0, 16-byte aligned base)
+ * w       uint32 [N, K*bits/32] row-major, packed low bits first: element j of row n is field
+ *         (j % (32/bits)) of word j / (32/bits)      (16-byte aligned base)
+ * scales  bf16 [N, K/group_size]
+ * biases  bf16 [N, K/group_size]
+ * y       bf16 [M, N], row stride ldy
+ * bits    4 or 8; group_size 64; K % 64 == 0.
+ *
+ * Replaces skinny_qmm.qmm(x2, weight, scales, biases, bits) (skinny_qmm.py:239-246), i.e. the
+ * `dspark_skinny_qmm` Metal kernel (skinny_qmm.py:56-171) and, outside its window, the stock
+ * mx.quantized_matmul reached through QuantizedLinear.__call__ (small_m_qmm.py:53, :71-80).
+ * Each output is computed independently of the other rows (row-count invariant, as the
+ * reference tests at tests/test_small_m_qmm.py:107-119).
+ */
+int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t K,
+                      const uint32_t* w, const void* scales, const void* biases,
+                      int64_t N, int bits, int group_size,
+                      void* y, int64_t ldy, dspark_stream stream);
+
+/* 0 if dspark_qmm_affine accepts this shape, else the dspark_status it would return.
+ * Mirrors skinny_qmm.fits (skinny_qmm.py:174-181) without launching. */
+int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int bits, int group_size);
+
+/* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size and M
+ * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,
+ * biases and y. Same numerics as separate dspark_qmm_affine calls (bitwise).
+ * Replaces the per-projection QuantizedLinear calls of one decoder layer
+ * (target.py:208-221 → mlx-lm DecoderLayer), which the reference launches one by one. */
+#define DSPARK_QMM_MAX_PROBLEMS 4
+typedef struct dspark_qmm_problem {
+  const void* x;
+  int64_t ldx;
+  const uint32_t* w;
+  const void* scales;
+  const void* biases;
+  void* y;
+  int64_t ldy;
+  int64_t N;
+  int64_t K;
+} dspark_qmm_problem;
+
+int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int count, int64_t M, int bits,
+                            int group_size, dspark_stream stream);
+
+/* ------------------------------------------------------------------ verify attention */
+
+/*
+ * out = softmax(scale * q k^T + mask) v for a few verify rows over a long KV cache.
+ *
+ * q        bf16 [B, Hq, Mq, D] contiguous
+ * k, v     bf16 [B, Hk, L_total, D] views with element strides k_strides = {batch, head, seq}
+ *          (the last dim must be contiguous; the cache capacity may exceed L_total)
+ * L_total  keys in the cache including the Mq rows being verified (already written)
+ * causal   1: row i (0-based within the Mq block) sees keys 0 .. L_total - Mq + i
+ *          0: every row sees every key
+ * tree_anc nullable uint32 [Mq]: tree-verify visibility — every key < L_total - Mq is seen;
+ *          key L_total - Mq + j is seen by row i iff bit j of tree_anc[i] is set (Mq <= 32).
+ *          Overrides `causal`.
+ * out      bf16 [B, Hq, Mq, D] contiguous
+ * workspace  device buffer of at least dspark_verify_attention_workspace(...) bytes
+ *            (fp32 split-KV partials); may be NULL when that size is 0.
+ * D in {64, 128}; Hq % Hk == 0; gqa * Mq <= 256.
+ *
+ * Replaces multirow_attn.multirow_sdpa(q, k, v, scale=, causal=, tree_anc=)
+ * (multirow_attn.py:223-259): the dspark_mra_p1 / _p1_tree / _p2 Metal kernels
+ * (multirow_attn.py:52-197).
+ */
+int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
+                            const void* k, const void* v, const int64_t k_strides[3],
+                            const int64_t v_strides[3], int64_t Hk, int64_t L_total, float scale,
+                            int causal, const uint32_t* tree_anc, void* out, void* workspace,
+                            size_t workspace_bytes, dspark_stream stream);
+
+/* Workspace bytes dspark_verify_attention needs for this shape (0 = none). */
+size_t dspark_verify_attention_workspace(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
+                                         int64_t L_total);
+
+/* Number of split-KV blocks the launch plan uses for this shape (for tests and reports).
+ * Mirrors multirow_attn.plan (multirow_attn.py:204-220) in spirit; the geometry is MI355X's. */
+int64_t dspark_verify_attention_blocks(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
+                                       int64_t L_total);
+
+/* ------------------------------------------------------------------ MoE */
+
+/*
+ * Router: gates = softmax(logits) computed in fp32 and rounded to bf16 (mlx
+ * softmax(precise=True) keeps the input dtype); top-k by (gate desc, expert id asc);
+ * scores = the selected gates, renormalized to sum 1 when renorm != 0 (norm_topk_prob),
+ * rounded to bf16. Outputs:
+ *   inds    int32 [M, k]    selected experts, in selection order (largest gate first)
+ *   scores  bf16  [M, k]
+ *   expert_offsets  int32 [E + 1] (nullable): bucket boundaries of the (token, slot) pairs
+ *                   sorted by expert, then by pair id t*k + j
+ *   sorted_pairs    int32 [M * k] (nullable): pair ids t*k + j in that sorted order
+ *   pair_pos        int32 [M * k] (nullable): inverse of sorted_pairs
+ * Requires 1 <= k <= 32, k <= E <= 1024.
+ * Replaces mlx-lm's SparseMoeBlock routing (softmax → argpartition → take_along_axis →
+ * renormalize; mlx-lm qwen3_moe, third-party, not vendored in the reference) and SwitchGLU's
+ * sort of the (token, expert) pairs (mlx-lm switch_layers).
+ */
+int dspark_moe_route_topk(const void* logits, int64_t M, int64_t E, int64_t k, int renorm,
+                          int32_t* inds, void* scores, int32_t* expert_offsets,
+                          int32_t* sorted_pairs, int32_t* pair_pos, dspark_stream stream);
+
+/*
+ * Grouped affine qmm over expert-sorted rows (mx.gather_qmm(x, w, s, b, rhs_indices=...,
+ * transpose=True, sorted_indices=True)):
+ *   y[p, :] = x[row_index[p], :] @ dequant(w[e])^T   for expert_offsets[e] <= p < expert_offsets[e+1]
+ * x       bf16 [*, K] (row stride ldx); row_index int32 [P] (nullable = identity)
+ * w       uint32 [E, N, K*bits/32]; scales/biases bf16 [E, N, K/64]
+ * y       bf16 [P, N] (row stride ldy), P = expert_offsets[E]
+ * Rows are streamed per expert, so each selected expert's weights are read once.
+ */
+int dspark_gather_qmm(const void* x, int64_t ldx, int64_t K, const int32_t* row_index,
+                      const int32_t* expert_offsets, int64_t E, int64_t P_max,
+                      const uint32_t* w, const void* scales, const void* biases, int64_t N,
+                      int bits, int group_size, void* y, int64_t ldy, dspark_stream stream);
+
+/*
+ * The whole routed-expert MLP of one MoE block for M tokens (SwitchGLU + score combine):
+ *   route (dspark_moe_route_topk) → gate/up gather_qmm with h = silu(gate) * up (bf16)
+ *   → down gather_qmm → out[t] = sum_j bf16(scores[t,j] * y[t,j]) (fp32 sum, slot order).
+ * x bf16 [M, H]; logits bf16 [M, E]; w_gate/w_up uint32 [E, I, H*bits/32];
+ * w_down uint32 [E, H, I*bits/32]; s_*, b_* bf16 [E, rows, cols/64]; out bf16 [M, H].
+ * inds/scores (outputs, nullable) receive the routing.
+ * workspace >= dspark_moe_workspace(M, H, I, E, k) bytes.
+ * Replaces mlx-lm SwitchGLU.__call__ / QuantizedSwitchLinear (third-party; §3.3 of the
+ * reference's call stack) for the A3B targets the reference routes (load.py:111-123).
+ */
+int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t H, int64_t I,
+                          int64_t E, int64_t k, int renorm,
+                          const uint32_t* w_gate, const void* s_gate, const void* b_gate,
+                          const uint32_t* w_up, const void* s_up, const void* b_up,
+                          const uint32_t* w_down, const void* s_down, const void* b_down,
+                          int bits, int group_size, void* out, int32_t* inds, void* scores,
+                          void* workspace, size_t workspace_bytes, dspark_stream stream);
+
+size_t dspark_moe_workspace(int64_t M, int64_t H, int64_t I, int64_t E, int64_t k);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSPARK_H_ */

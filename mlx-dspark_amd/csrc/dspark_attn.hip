@@ -1,0 +1,390 @@
+// Multi-row causal GQA verify attention for gfx950 (MI355X).
+//
+// Semantics (multirow_attn.py:52-178, :223-259): q [B, Hq, Mq, D] is viewed per KV head as
+// R = gqa * Mq rows (row r = g*Mq + i is query head hk*gqa + g at block position i). K/V hold
+// L keys (prefix + the Mq verify rows, already written). Causal: row i sees keys
+// 0 .. L - Mq + i. Softmax in the exp2 domain with fp32 running max m (init -1e30) and sum l;
+// P is rounded to bf16 for the P.V product (multirow_attn.py:131-140); partials of the
+// split-KV blocks are merged as out = sum 2^(m_j - M) o_j / sum 2^(m_j - M) l_j
+// (multirow_attn.py:162-178).
+//
+// MI355X mapping:
+//   * grid = (B*Hk, NB key blocks, row groups); a 256-thread workgroup (4 waves) owns one KV
+//     head's key block and up to 4 row tiles of 16 rows (all gqa*Mq rows of the head when
+//     they fit), so each K/V byte is read from HBM once per workgroup and shared by every
+//     query head of the GQA group.
+//   * 64-key tiles are staged through LDS with register double buffering: K row-major
+//     (padded rows), V transposed (key-contiguous, 8-key blocks XOR-swizzled by d) because the
+//     P.V MFMA reduces over keys.
+//   * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16. Computing the transposed
+//     scores leaves each lane holding 8 keys of one query row, which is exactly the B operand
+//     of the P.V MFMA — no shuffle of P.
+//   * row max: 2 cross-lane xor-shuffles per tile; the row sum stays lane-partial until the end.
+#include "dspark_common.h"
+
+namespace dspark {
+namespace {
+
+constexpr int KT = 64;      // keys per LDS tile
+constexpr int WAVES = 4;    // row tiles per workgroup
+constexpr int THREADS = 64 * WAVES;
+
+struct AttnArgs {
+  const u16* q;
+  const u16* k;
+  const u16* v;
+  const u32* anc;
+  float* opart;
+  float* mpart;
+  float* lpart;
+  u16* out;
+  long ksb, ksh, kss;
+  long vsb, vsh, vss;
+  int Hq, Hk, Mq, L;
+  int gqa, R, RT, RP;
+  int chunk, NB;
+  float scale_log2;
+  int causal;
+};
+
+// position of key (0..63) inside a tile's transposed V row: the 8 keys one lane needs for one
+// P.V MFMA (keys 32u + 4q + {0..3} and 32u + 16 + 4q + {0..3}) are made contiguous.
+__device__ __forceinline__ int vt_pos(int key) {
+  const int u = key >> 5, h = (key >> 4) & 1, qq = (key >> 2) & 3, i = key & 3;
+  return (u << 5) | (qq << 3) | (h << 2) | i;
+}
+// swizzled element offset of (d, pos) in the transposed V tile (row pitch KT)
+__device__ __forceinline__ int vt_off(int d, int pos) {
+  return d * KT + ((((pos >> 3) ^ (d >> 1) ^ (d >> 3)) & 7) << 3) + (pos & 7);
+}
+
+template <int D, bool TREE>
+__global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
+  constexpr int KP = D + 8;           // padded K row (elements)
+  constexpr int DC = D / 8;           // 16-byte chunks per key row
+  constexpr int LOADS = KT * DC / THREADS;  // 16-byte K chunks per thread per tile
+  constexpr int NDC = D / 32;         // d-chunks of the S MFMA
+  constexpr int NDT = D / 16;         // d-tiles of the O MFMA
+  __shared__ __attribute__((aligned(16))) u16 ks_lds[KT * KP];
+  __shared__ __attribute__((aligned(16))) u16 vt_lds[D * KT];
+
+  const int bh = blockIdx.x;
+  const int b = bh / a.Hk, hk = bh % a.Hk;
+  const int blk = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q4 = lane >> 4;
+  const int rt = blockIdx.z * WAVES + wave;
+  const bool active = rt < a.RT;
+
+  const int L = a.L;
+  const int k0 = blk * a.chunk;
+  const int k1 = min(L, k0 + a.chunk);
+
+  const u16* kbase = a.k + b * a.ksb + hk * a.ksh;
+  const u16* vbase = a.v + b * a.vsb + hk * a.vsh;
+
+  // ---- this lane's query row (B operand of S^T = K Q^T)
+  const int rr = min(rt * 16 + c16, a.R - 1);
+  const int qi = rr % a.Mq;
+  const u16* qrow = a.q + ((long)(b * a.Hq + hk * a.gqa) * a.Mq + rr) * D;
+  u32x4_t qf[NDC];
+#pragma unroll
+  for (int c = 0; c < NDC; ++c) qf[c] = ldg128(qrow + 32 * c + 8 * q4);
+  const int kmax = a.causal ? (L - a.Mq + qi) : (L - 1);
+  const u32 anc = TREE ? a.anc[qi] : 0u;
+  const int tail0 = L - a.Mq;  // first key of the verify block
+
+  f32x4_t o[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -1e30f, l = 0.f;
+
+  // ---- cooperative tile loads into registers.
+  // K: 16-byte chunk c = tid + THREADS*j -> (key c / DC, d-chunk c % DC), stored row-major.
+  // V: thread (key quad vkq = tid & 15, d-chunk vdc = tid >> 4) loads keys 4vkq..4vkq+3 and
+  //    writes the transposed tile as 8 ds_write_b64 (4 keys of one d each); odd d-chunks walk
+  //    their 8 d-rows in pair-swapped order so each half-wave covers all 64 LDS banks.
+  const bool vthread = tid < 16 * DC;
+  const int vkq = tid & 15, vdc = tid >> 4;
+  u32x4_t kreg[LOADS], vreg[4];
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int c = tid + THREADS * j;
+      const int key = min(kt + c / DC, L - 1);
+      kreg[j] = ldg128(kbase + (long)key * a.kss + 8 * (c % DC));
+    }
+    if (vthread) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = min(kt + 4 * vkq + j, L - 1);
+        vreg[j] = ldg128(vbase + (long)key * a.vss + 8 * vdc);
+      }
+    }
+  };
+  // element (e ^ (vdc & 1)) of each 8-wide chunk: low half-word of word e >> 1 when that index
+  // is even, high half-word when odd
+  const u32 sel_lo = 0x05040100u, sel_hi = 0x07060302u;
+  const u32 vsel_even = (vdc & 1) ? sel_hi : sel_lo;  // e even
+  const u32 vsel_odd = (vdc & 1) ? sel_lo : sel_hi;   // e odd
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int c = tid + THREADS * j;
+      *reinterpret_cast<u32x4_t*>(&ks_lds[(c / DC) * KP + 8 * (c % DC)]) = kreg[j];
+    }
+    if (vthread) {
+      const int pos = vt_pos(4 * vkq);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * vdc + (e ^ (vdc & 1));
+        const int wd = e >> 1;
+        const u32 vsel = (e & 1) ? vsel_odd : vsel_even;
+        const u32x2_t pr = {__builtin_amdgcn_perm(vreg[1][wd], vreg[0][wd], vsel),
+                            __builtin_amdgcn_perm(vreg[3][wd], vreg[2][wd], vsel)};
+        *reinterpret_cast<u32x2_t*>(&vt_lds[vt_off(d, pos)]) = pr;
+      }
+    }
+  };
+
+  if (k0 < k1) load_tile(k0);
+  for (int kt = k0; kt < k1; kt += KT) {
+    __syncthreads();  // previous tile fully consumed
+    store_tile();
+    __syncthreads();
+    if (kt + KT < k1) load_tile(kt + KT);
+    if (!active) continue;
+
+    // S^T[key][row] for 4 subtiles of 16 keys
+    f32x4_t s[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      s[ks] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(&ks_lds[(16 * ks + c16) * KP + 32 * c + 8 * q4]);
+        s[ks] = mfma16x16x32(kf, qf[c], s[ks]);
+      }
+    }
+    // mask + scale, row max
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kt + 16 * ks + 4 * q4 + i;
+        bool vis = key < k1;
+        if (TREE)
+          vis = vis && (key < tail0 || ((anc >> ((unsigned)(key - tail0) & 31u)) & 1u));
+        else
+          vis = vis && key <= kmax;
+        const float sv = vis ? s[ks][i] * a.scale_log2 : -INFINITY;
+        s[ks][i] = sv;
+        mloc = fmaxf(mloc, sv);
+      }
+    mloc = fmaxf(mloc, shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+    const float mn = fmaxf(m, mloc);
+    const float alpha = exp2f(m - mn);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = exp2f(s[ks][i] - mn);
+        s[ks][i] = p;
+        ps += p;
+      }
+    l = l * alpha + ps;
+    u32x4_t pk[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      pk[u] = u32x4_t{pack_bf16x2(s[2 * u][0], s[2 * u][1]), pack_bf16x2(s[2 * u][2], s[2 * u][3]),
+                      pack_bf16x2(s[2 * u + 1][0], s[2 * u + 1][1]), pack_bf16x2(s[2 * u + 1][2], s[2 * u + 1][3])};
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      o[t] *= alpha;
+      const int d = 16 * t + c16;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(&vt_lds[vt_off(d, 32 * u + 8 * q4)]);
+        o[t] = mfma16x16x32(vf, pk[u], o[t]);
+      }
+    }
+  }
+  if (!active) return;
+
+  // ---- finalize: lane (row c16, quarter q4) holds O^T[16t + 4q4 + i][row]
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+  const int row = rt * 16 + c16;
+  if (row >= a.R) return;
+  if (a.NB == 1) {
+    const float inv = 1.0f / l;
+    u16* orow = a.out + ((long)(b * a.Hq + hk * a.gqa) * a.Mq + row) * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      u32x2_t pk2 = {pack_bf16x2(o[t][0] * inv, o[t][1] * inv), pack_bf16x2(o[t][2] * inv, o[t][3] * inv)};
+      *reinterpret_cast<u32x2_t*>(orow + 16 * t + 4 * q4) = pk2;
+    }
+    return;
+  }
+  const long pbase = ((long)bh * a.NB + blk) * a.RP + row;
+  float* op = a.opart + pbase * D;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) *reinterpret_cast<f32x4_t*>(op + 16 * t + 4 * q4) = o[t];
+  if (q4 == 0) {
+    a.mpart[pbase] = m;
+    a.lpart[pbase] = l;
+  }
+}
+
+// out[row, d] = sum_j 2^(m_j - M) o_j[row, d] / sum_j 2^(m_j - M) l_j[row]
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.Hk, hk = bh % a.Hk;
+  const int idx = blockIdx.y * 256 + threadIdx.x;
+  const int row = idx / D, d = idx % D;
+  if (row >= a.R) return;
+  const long base = (long)bh * a.NB * a.RP + row;
+  float M = -1e30f;
+  for (int j = 0; j < a.NB; ++j) M = fmaxf(M, a.mpart[base + (long)j * a.RP]);
+  float num = 0.f, den = 0.f;
+  for (int j = 0; j < a.NB; ++j) {
+    const long pj = base + (long)j * a.RP;
+    const float w = exp2f(a.mpart[pj] - M);
+    den += w * a.lpart[pj];
+    num += w * a.opart[pj * D + d];
+  }
+  a.out[((long)(b * a.Hq + hk * a.gqa) * a.Mq + row) * D + d] = f2bf(num / den);
+}
+
+struct Plan {
+  int R, RT, RP, NRG, chunk, NB;
+};
+
+Plan make_plan(long B, long Hq, long Hk, long Mq, long L) {
+  Plan p{};
+  p.R = (int)((Hq / Hk) * Mq);
+  p.RT = (p.R + 15) / 16;
+  p.RP = p.RT * 16;
+  p.NRG = (p.RT + WAVES - 1) / WAVES;
+  // ~2 workgroups per CU (256 CUs) on long caches; at least 4 tiles (256 keys) per block so
+  // the fp32 partials stay a small fraction of the KV stream.
+  const long heads = B * Hk * p.NRG;
+  const long target = 512;
+  long nb = (target + heads - 1) / heads;
+  const long max_nb = (L + 4 * KT - 1) / (4 * KT);
+  if (nb > max_nb) nb = max_nb;
+  if (nb < 1) nb = 1;
+  long chunk = (L + nb - 1) / nb;
+  chunk = ((chunk + KT - 1) / KT) * KT;
+  p.chunk = (int)chunk;
+  p.NB = (int)((L + chunk - 1) / chunk);
+  return p;
+}
+
+size_t workspace_bytes(const Plan& p, long B, long Hk, long D) {
+  if (p.NB <= 1) return 0;
+  const size_t rows = (size_t)B * Hk * p.NB * p.RP;
+  return rows * D * sizeof(float) + 2 * rows * sizeof(float);
+}
+
+int check_shape(long B, long Hq, long Mq, long D, long Hk, long L) {
+  if (B < 1 || Hq < 1 || Hk < 1 || Mq < 1 || L < 1)
+    return fail(DSPARK_ERR_SHAPE, "verify_attention: B=%ld Hq=%ld Hk=%ld Mq=%ld L=%ld", B, Hq, Hk, Mq, L);
+  if (Hq % Hk) return fail(DSPARK_ERR_SHAPE, "verify_attention: Hq=%ld not a multiple of Hk=%ld", Hq, Hk);
+  if (D != 64 && D != 128) return fail(DSPARK_ERR_SHAPE, "verify_attention: head_dim %ld (64 or 128 supported)", D);
+  if (Mq > L) return fail(DSPARK_ERR_SHAPE, "verify_attention: Mq=%ld > L=%ld", Mq, L);
+  if ((Hq / Hk) * Mq > 256) return fail(DSPARK_ERR_SHAPE, "verify_attention: gqa*Mq=%ld > 256", (Hq / Hk) * Mq);
+  if (L >= (1L << 30) || B * Hk >= (1L << 20)) return fail(DSPARK_ERR_SHAPE, "verify_attention: too large");
+  return DSPARK_OK;
+}
+
+}  // namespace
+}  // namespace dspark
+
+using namespace dspark;
+
+extern "C" size_t dspark_verify_attention_workspace(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
+                                                    int64_t L_total) {
+  if (check_shape(B, Hq, Mq, D, Hk, L_total)) return 0;
+  return workspace_bytes(make_plan(B, Hq, Hk, Mq, L_total), B, Hk, D);
+}
+
+extern "C" int64_t dspark_verify_attention_blocks(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
+                                                  int64_t L_total) {
+  if (check_shape(B, Hq, Mq, D, Hk, L_total)) return -1;
+  return make_plan(B, Hq, Hk, Mq, L_total).NB;
+}
+
+extern "C" int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D, const void* k,
+                                       const void* v, const int64_t k_strides[3], const int64_t v_strides[3],
+                                       int64_t Hk, int64_t L_total, float scale, int causal,
+                                       const uint32_t* tree_anc, void* out, void* workspace, size_t workspace_bytes_,
+                                       dspark_stream stream) {
+  if (!q || !k || !v || !k_strides || !v_strides || !out) return fail(DSPARK_ERR_ARG, "verify_attention: null pointer");
+  int st = check_shape(B, Hq, Mq, D, Hk, L_total);
+  if (st) return st;
+  if (tree_anc && Mq > 32) return fail(DSPARK_ERR_SHAPE, "verify_attention: tree mask needs Mq <= 32");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 8))
+    return fail(DSPARK_ERR_ALIGN, "verify_attention: q/k/v must be 16-byte aligned, out 8-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    if ((k_strides[i] % 8) || (v_strides[i] % 8) || k_strides[i] < 0 || v_strides[i] < 0)
+      return fail(DSPARK_ERR_ALIGN, "verify_attention: K/V strides must be non-negative multiples of 8 elements");
+  const Plan p = make_plan(B, Hq, Hk, Mq, L_total);
+  const size_t need = workspace_bytes(p, B, Hk, D);
+  if (need && (!workspace || workspace_bytes_ < need))
+    return fail(DSPARK_ERR_WORKSPACE, "verify_attention: workspace %zu < %zu bytes", workspace_bytes_, need);
+  if (need && !aligned(workspace, 16)) return fail(DSPARK_ERR_ALIGN, "verify_attention: workspace must be 16-byte aligned");
+
+  AttnArgs a{};
+  a.q = static_cast<const u16*>(q);
+  a.k = static_cast<const u16*>(k);
+  a.v = static_cast<const u16*>(v);
+  a.anc = tree_anc;
+  a.out = static_cast<u16*>(out);
+  a.ksb = k_strides[0];
+  a.ksh = k_strides[1];
+  a.kss = k_strides[2];
+  a.vsb = v_strides[0];
+  a.vsh = v_strides[1];
+  a.vss = v_strides[2];
+  a.Hq = (int)Hq;
+  a.Hk = (int)Hk;
+  a.Mq = (int)Mq;
+  a.L = (int)L_total;
+  a.gqa = (int)(Hq / Hk);
+  a.R = p.R;
+  a.RT = p.RT;
+  a.RP = p.RP;
+  a.chunk = p.chunk;
+  a.NB = p.NB;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.causal = causal ? 1 : 0;
+  if (need) {
+    const size_t rows = (size_t)B * Hk * p.NB * p.RP;
+    a.opart = static_cast<float*>(workspace);
+    a.mpart = a.opart + rows * D;
+    a.lpart = a.mpart + rows;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid1((unsigned)(B * Hk), (unsigned)p.NB, (unsigned)p.NRG);
+  const bool tree = tree_anc != nullptr;
+  if (D == 128) {
+    if (tree) hipLaunchKernelGGL((attn_p1_kernel<128, true>), grid1, dim3(THREADS), 0, s, a);
+    else hipLaunchKernelGGL((attn_p1_kernel<128, false>), grid1, dim3(THREADS), 0, s, a);
+  } else {
+    if (tree) hipLaunchKernelGGL((attn_p1_kernel<64, true>), grid1, dim3(THREADS), 0, s, a);
+    else hipLaunchKernelGGL((attn_p1_kernel<64, false>), grid1, dim3(THREADS), 0, s, a);
+  }
+  st = check_launch("verify_attention(p1)");
+  if (st || p.NB == 1) return st;
+  const dim3 grid2((unsigned)(B * Hk), (unsigned)((p.R * D + 255) / 256));
+  if (D == 128) hipLaunchKernelGGL((attn_combine_kernel<128>), grid2, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((attn_combine_kernel<64>), grid2, dim3(256), 0, s, a);
+  return check_launch("verify_attention(combine)");
+}

@@ -1,0 +1,68 @@
+// Shared helpers for the gfx950 kernels: vector types, bf16 conversions, the MFMA wrapper,
+// and the host-side status/error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dspark.h"
+
+namespace dspark {
+
+using u16 = uint16_t;
+using u32 = uint32_t;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef u32 u32x4_t __attribute__((ext_vector_type(4)));
+typedef u32 u32x2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- device helpers
+
+__device__ __forceinline__ float bf2f(u32 bits16) { return __builtin_bit_cast(float, bits16 << 16); }
+
+__device__ __forceinline__ u16 f2bf(float f) {
+  // round-to-nearest-even (v_cvt_pk_bf16_f32)
+  return __builtin_bit_cast(u16, (__bf16)f);
+}
+
+__device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
+  bf16x2_t p = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(u32, p);
+}
+
+// D = A(16 x 32) * B(32 x 16) + C, bf16 operands, fp32 accumulate.
+// Operand layout (wave64): lane l supplies row/column (l & 15) and the 8 reduction slots
+// 8*(l >> 4) .. +7; any consistent assignment of reduction indices to (l >> 4, element)
+// across A and B gives the same sum. Output: lane l holds D[4*(l >> 4) + r][l & 15], r = 0..3.
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4_t ldg128(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+__device__ __forceinline__ u32x2_t ldg64(const void* p) {
+  return *reinterpret_cast<const u32x2_t*>(p);
+}
+
+// Wave64 cross-lane exchange (ds_bpermute, no LDS storage).
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  const int lane = __lane_id();
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
+}
+
+// ---------------------------------------------------------------- host helpers
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// Turns a failed launch into DSPARK_ERR_LAUNCH with the HIP error text.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace dspark

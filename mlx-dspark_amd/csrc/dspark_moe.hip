@@ -1,0 +1,422 @@
+// MoE top-k routing, expert bucketing and grouped expert qmm for gfx950 (MI355X).
+//
+// The reference routes A3B targets through mlx-lm's SparseMoeBlock + SwitchGLU (third-party,
+// not vendored; call stack in the reference's load.py:111-123 routing and roofline.py:190-245
+// accounting):
+//     gates  = softmax(router(x), precise=True)            (fp32 math, bf16 result)
+//     inds   = argpartition(-gates, k-1)[..., :k]          (unordered top-k)
+//     scores = take_along_axis(gates, inds); scores /= scores.sum(-1)
+//     y      = SwitchGLU(x, inds)   # pairs sorted by expert when inds.size >= 64, gather_qmm
+//     out    = (y * scores[..., None]).sum(-2)
+// Tie rule used here (argpartition leaves it unspecified): experts are ranked by router logit
+// (descending), then expert id (ascending). Softmax is monotone, so this is one of the orders
+// argpartition may return on the bf16 gates, and it is bit-reproducible.
+//
+// MI355X mapping: one tiny workgroup routes all M tokens and builds the expert buckets
+// (counting sort, stable in pair id). The grouped qmm launches one workgroup per
+// (expert, 16-feature tile); workgroups of unselected experts exit at once, every selected
+// expert's weight tile is streamed once for all of its tokens (<= 16 at verify widths).
+#include "dspark_qmm_core.h"
+
+namespace dspark {
+namespace {
+
+constexpr int kRouteThreads = 256;
+constexpr int kGatherWaves = 4;
+
+struct RouteArgs {
+  const u16* logits;
+  int* inds;
+  u16* scores;
+  int* offsets;
+  int* sorted;
+  int* pos;
+  int M, E, k, renorm;
+};
+
+__device__ __forceinline__ float bf16r(float f) { return bf2f(f2bf(f)); }
+
+// max by (value desc, id asc)
+__device__ __forceinline__ void argbest(float& v, int& id, float v2, int id2) {
+  if (v2 > v || (v2 == v && id2 < id)) {
+    v = v2;
+    id = id2;
+  }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArgs a) {
+  extern __shared__ int lds[];
+  int* pair_e = lds;                 // [M*k]
+  int* counts = lds + a.M * a.k;     // [E + 1]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int P = a.M * a.k;
+  constexpr int NPL = 16;  // experts per lane (E <= 1024)
+
+  for (int t = wave; t < a.M; t += kRouteThreads / 64) {
+    float xv[NPL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int e = lane + 64 * i;
+      const float lv = (e < a.E) ? bf2f(a.logits[(long)t * a.E + e]) : -INFINITY;
+      xv[i] = (lv == lv) ? lv : -INFINITY;  // NaN ranks last, so a valid expert is always chosen
+      mx = fmaxf(mx, xv[i]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+      if (lane + 64 * i < a.E) sum += expf(xv[i] - mx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
+    // all lanes now hold the same fp32 sum (same xor tree on every lane)
+    u32 taken = 0;
+    float gsel[32];
+    float gsum = 0.f;
+    for (int j = 0; j < a.k; ++j) {
+      float bv = -INFINITY;
+      int bid = 1 << 30;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const int e = lane + 64 * i;
+        if (e < a.E && !((taken >> i) & 1u)) argbest(bv, bid, xv[i], e);
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float v2 = shfl_xor(bv, o);
+        const int id2 = __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, bid);
+        argbest(bv, bid, v2, id2);
+      }
+      if ((bid & 63) == lane) taken |= 1u << (bid >> 6);
+      const float g = bf16r(expf(bv - mx) / sum);
+      gsel[j] = g;
+      gsum += g;
+      if (lane == 0) a.inds[t * a.k + j] = bid;
+      if (lane == 0) pair_e[t * a.k + j] = bid;
+    }
+    const float denom = bf16r(gsum);
+    if (lane == 0) {
+      for (int j = 0; j < a.k; ++j) {
+        const float s = a.renorm ? bf16r(gsel[j] / denom) : gsel[j];
+        a.scores[t * a.k + j] = f2bf(s);
+      }
+    }
+  }
+  if (!a.offsets) return;
+  // ---- bucket the (token, slot) pairs by expert, stable in pair id
+  for (int e = threadIdx.x; e <= a.E; e += kRouteThreads) counts[e] = 0;
+  __syncthreads();
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) atomicAdd(&counts[pair_e[p]], 1);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int e = 0; e < a.E; ++e) {
+      const int c = counts[e];
+      counts[e] = run;
+      a.offsets[e] = run;
+      run += c;
+    }
+    counts[a.E] = run;
+    a.offsets[a.E] = run;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
+    const int e = pair_e[p];
+    int r = 0;
+    for (int p2 = 0; p2 < p; ++p2) r += (pair_e[p2] == e);
+    const int dst = counts[e] + r;
+    if (a.sorted) a.sorted[dst] = p;
+    if (a.pos) a.pos[p] = dst;
+  }
+}
+
+// ---------------------------------------------------------------- grouped expert qmm
+
+enum GatherMode { kPlain = 0, kSwiGLU = 1 };
+
+struct GatherArgs {
+  const u16* x;
+  const int* row_index;  // nullable: x row of sorted position p (else p)
+  const int* offsets;    // [E + 1]
+  const u32* w0;         // [E, N, K*bits/32] (gate for SwiGLU)
+  const u16* s0;
+  const u16* b0;
+  const u32* w1;         // up (SwiGLU only)
+  const u16* s1;
+  const u16* b1;
+  u16* y;                // [P, N]
+  long ldx, ldy;
+  int K, N, row_div, P_max;
+};
+
+template <int BITS, int MODE, int CH>
+__global__ __launch_bounds__(64 * kGatherWaves) void gather_qmm_kernel(const GatherArgs a) {
+  constexpr int W = kGatherWaves;
+  constexpr int NT = (MODE == kSwiGLU) ? 2 : 1;
+  const int e = blockIdx.x;
+  const int p0 = a.offsets[e], p1 = min(a.offsets[e + 1], a.P_max);
+  if (p0 >= p1) return;
+  const int n_base = blockIdx.y * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int G = a.K >> 6;
+  const int g0 = (wave * G) / W, g1 = ((wave + 1) * G) / W;
+  const long wstride = (long)a.N * (a.K * BITS / 32);
+  const long sstride = (long)a.N * G;
+
+  const int n = min(n_base + c16, a.N - 1);
+  const u32* wr[NT];
+  const u16* sr[NT];
+  const u16* br[NT];
+  wr[0] = wrow_ptr<BITS>(a.w0 + e * wstride, n, a.K, q);
+  sr[0] = a.s0 + e * sstride + (long)n * G;
+  br[0] = a.b0 + e * sstride + (long)n * G;
+  if constexpr (MODE == kSwiGLU) {
+    wr[NT - 1] = wrow_ptr<BITS>(a.w1 + e * wstride, n, a.K, q);
+    sr[NT - 1] = a.s1 + e * sstride + (long)n * G;
+    br[NT - 1] = a.b1 + e * sstride + (long)n * G;
+  }
+  __shared__ float red[W][NT][256];
+  for (int mb = p0; mb < p1; mb += 16) {
+    const int p = min(mb + c16, p1 - 1);
+    const int src = (a.row_index ? a.row_index[p] : p) / a.row_div;
+    const u16* xr = a.x + (long)src * a.ldx + 16 * q;
+    f32x4_t acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    qmm_wave_partial<BITS, NT, CH>(xr, wr, sr, br, g0, g1, acc);
+    __syncthreads();  // previous m-tile's reduction has read red
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][j][(4 * q + r) * 16 + c16] = acc[j][r];
+    __syncthreads();
+    for (int t = threadIdx.x; t < 256; t += 64 * W) {
+      const int m = t >> 4, nn = t & 15;
+      float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) {
+        v0 += red[ww][0][t];
+        if constexpr (MODE == kSwiGLU) v1 += red[ww][NT - 1][t];
+      }
+      const int pp = mb + m, nf = n_base + nn;
+      if (pp < p1 && nf < a.N) {
+        float out = v0;
+        if constexpr (MODE == kSwiGLU) {
+          // h = silu(gate) * up with the bf16 rounding of each elementwise op
+          const float g = bf16r(v0), u = bf16r(v1);
+          const float sg = bf16r(1.0f / (1.0f + expf(-g)));
+          out = bf16r(g * sg) * u;
+        }
+        a.y[(long)pp * a.ldy + nf] = f2bf(out);
+      }
+    }
+  }
+}
+
+// out[t, n] = sum_j bf16(scores[t, j] * y[pos[t*k + j], n])   (fp32 sum in slot order)
+__global__ __launch_bounds__(256) void moe_combine_kernel(const u16* __restrict__ y, const int* __restrict__ pos,
+                                                          const u16* __restrict__ scores, u16* __restrict__ out,
+                                                          int H, int k) {
+  const int t = blockIdx.x;
+  const int n = blockIdx.y * 256 + threadIdx.x;
+  if (n >= H) return;
+  float acc = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int p = pos[t * k + j];
+    acc += bf16r(bf2f(scores[t * k + j]) * bf2f(y[(long)p * H + n]));
+  }
+  out[(long)t * H + n] = f2bf(acc);
+}
+
+int check_route(long M, long E, long k) {
+  if (M < 1 || E < 1 || k < 1) return fail(DSPARK_ERR_SHAPE, "moe_route: M=%ld E=%ld k=%ld", M, E, k);
+  if (k > 32 || k > E || E > 1024) return fail(DSPARK_ERR_SHAPE, "moe_route: need 1 <= k <= 32, k <= E <= 1024 (E=%ld k=%ld)", E, k);
+  if (M * k > 8192) return fail(DSPARK_ERR_SHAPE, "moe_route: M*k=%ld > 8192", M * k);
+  return DSPARK_OK;
+}
+
+int launch_route(const RouteArgs& a, hipStream_t s) {
+  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + a.E + 1);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), lds, s, a);
+  return check_launch("moe_route_topk");
+}
+
+template <int MODE>
+int launch_gather(const GatherArgs& a, int E, int bits, hipStream_t s) {
+  const dim3 grid((unsigned)E, (unsigned)((a.N + 15) / 16));
+  constexpr int CH = 4;
+  if (bits == 4) hipLaunchKernelGGL((gather_qmm_kernel<4, MODE, CH>), grid, dim3(64 * kGatherWaves), 0, s, a);
+  else hipLaunchKernelGGL((gather_qmm_kernel<8, MODE, CH>), grid, dim3(64 * kGatherWaves), 0, s, a);
+  return check_launch(MODE == kSwiGLU ? "moe gate/up" : "gather_qmm");
+}
+
+int check_qmm_format(long K, long N, int bits, int group_size) {
+  if (bits != 4 && bits != 8) return fail(DSPARK_ERR_UNSUPPORTED, "gather_qmm: bits=%d", bits);
+  if (group_size != 64) return fail(DSPARK_ERR_UNSUPPORTED, "gather_qmm: group_size=%d", group_size);
+  if (K < 64 || K % 64 || N < 1) return fail(DSPARK_ERR_SHAPE, "gather_qmm: K=%ld N=%ld", K, N);
+  return DSPARK_OK;
+}
+
+inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+struct MoeWorkspace {
+  size_t offsets, sorted, pos, inds, scores, h, y, total;
+};
+
+MoeWorkspace moe_layout(long M, long H, long I, long E, long k) {
+  MoeWorkspace w{};
+  const size_t P = (size_t)M * k;
+  size_t o = 0;
+  w.offsets = o; o += align256(sizeof(int) * (E + 1));
+  w.sorted = o;  o += align256(sizeof(int) * P);
+  w.pos = o;     o += align256(sizeof(int) * P);
+  w.inds = o;    o += align256(sizeof(int) * P);
+  w.scores = o;  o += align256(sizeof(u16) * P);
+  w.h = o;       o += align256(sizeof(u16) * P * I);
+  w.y = o;       o += align256(sizeof(u16) * P * H);
+  w.total = o;
+  return w;
+}
+
+}  // namespace
+}  // namespace dspark
+
+using namespace dspark;
+
+extern "C" int dspark_moe_route_topk(const void* logits, int64_t M, int64_t E, int64_t k, int renorm, int32_t* inds,
+                                     void* scores, int32_t* expert_offsets, int32_t* sorted_pairs, int32_t* pair_pos,
+                                     dspark_stream stream) {
+  if (!logits || !inds || !scores) return fail(DSPARK_ERR_ARG, "moe_route: null pointer");
+  int st = check_route(M, E, k);
+  if (st) return st;
+  if ((sorted_pairs || pair_pos) && !expert_offsets)
+    return fail(DSPARK_ERR_ARG, "moe_route: sorted_pairs/pair_pos need expert_offsets");
+  RouteArgs a{};
+  a.logits = static_cast<const u16*>(logits);
+  a.inds = inds;
+  a.scores = static_cast<u16*>(scores);
+  a.offsets = expert_offsets;
+  a.sorted = sorted_pairs;
+  a.pos = pair_pos;
+  a.M = (int)M;
+  a.E = (int)E;
+  a.k = (int)k;
+  a.renorm = renorm ? 1 : 0;
+  return launch_route(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dspark_gather_qmm(const void* x, int64_t ldx, int64_t K, const int32_t* row_index,
+                                 const int32_t* expert_offsets, int64_t E, int64_t P_max, const uint32_t* w,
+                                 const void* scales, const void* biases, int64_t N, int bits, int group_size, void* y,
+                                 int64_t ldy, dspark_stream stream) {
+  if (!x || !expert_offsets || !w || !scales || !biases || !y) return fail(DSPARK_ERR_ARG, "gather_qmm: null pointer");
+  int st = check_qmm_format(K, N, bits, group_size);
+  if (st) return st;
+  if (E < 1 || P_max < 1) return fail(DSPARK_ERR_SHAPE, "gather_qmm: E=%lld P_max=%lld", (long long)E, (long long)P_max);
+  if (!aligned(x, 16) || ldx % 8 || ldx < K || !aligned(w, 16) || ldy < N)
+    return fail(DSPARK_ERR_ALIGN, "gather_qmm: x/w must be 16-byte aligned, ldx %% 8 == 0, ldx >= K, ldy >= N");
+  GatherArgs a{};
+  a.x = static_cast<const u16*>(x);
+  a.row_index = row_index;
+  a.offsets = expert_offsets;
+  a.w0 = w;
+  a.s0 = static_cast<const u16*>(scales);
+  a.b0 = static_cast<const u16*>(biases);
+  a.y = static_cast<u16*>(y);
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.K = (int)K;
+  a.N = (int)N;
+  a.row_div = 1;
+  a.P_max = (int)P_max;
+  return launch_gather<kPlain>(a, (int)E, bits, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t dspark_moe_workspace(int64_t M, int64_t H, int64_t I, int64_t E, int64_t k) {
+  if (check_route(M, E, k)) return 0;
+  return moe_layout(M, H, I, E, k).total;
+}
+
+extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t H, int64_t I, int64_t E,
+                                     int64_t k, int renorm, const uint32_t* w_gate, const void* s_gate,
+                                     const void* b_gate, const uint32_t* w_up, const void* s_up, const void* b_up,
+                                     const uint32_t* w_down, const void* s_down, const void* b_down, int bits,
+                                     int group_size, void* out, int32_t* inds, void* scores, void* workspace,
+                                     size_t workspace_bytes, dspark_stream stream) {
+  if (!x || !logits || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up || !w_down || !s_down || !b_down || !out)
+    return fail(DSPARK_ERR_ARG, "moe_switch_glu: null pointer");
+  int st = check_route(M, E, k);
+  if (st) return st;
+  if ((st = check_qmm_format(H, I, bits, group_size))) return st;
+  if ((st = check_qmm_format(I, H, bits, group_size))) return st;
+  if (!aligned(x, 16) || !aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(out, 2))
+    return fail(DSPARK_ERR_ALIGN, "moe_switch_glu: x and packed weights must be 16-byte aligned");
+  const MoeWorkspace L = moe_layout(M, H, I, E, k);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(DSPARK_ERR_WORKSPACE, "moe_switch_glu: workspace %zu < %zu bytes", workspace_bytes, L.total);
+  if (!aligned(workspace, 256)) return fail(DSPARK_ERR_ALIGN, "moe_switch_glu: workspace must be 256-byte aligned");
+  char* ws = static_cast<char*>(workspace);
+  int* offsets = reinterpret_cast<int*>(ws + L.offsets);
+  int* sorted = reinterpret_cast<int*>(ws + L.sorted);
+  int* pos = reinterpret_cast<int*>(ws + L.pos);
+  int* inds_ws = inds ? inds : reinterpret_cast<int*>(ws + L.inds);
+  u16* scores_ws = scores ? static_cast<u16*>(scores) : reinterpret_cast<u16*>(ws + L.scores);
+  u16* h = reinterpret_cast<u16*>(ws + L.h);
+  u16* ypair = reinterpret_cast<u16*>(ws + L.y);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  RouteArgs r{};
+  r.logits = static_cast<const u16*>(logits);
+  r.inds = inds_ws;
+  r.scores = scores_ws;
+  r.offsets = offsets;
+  r.sorted = sorted;
+  r.pos = pos;
+  r.M = (int)M;
+  r.E = (int)E;
+  r.k = (int)k;
+  r.renorm = renorm ? 1 : 0;
+  if ((st = launch_route(r, s))) return st;
+
+  const int P = (int)(M * k);
+  GatherArgs g{};
+  g.x = static_cast<const u16*>(x);
+  g.row_index = sorted;
+  g.offsets = offsets;
+  g.w0 = w_gate;
+  g.s0 = static_cast<const u16*>(s_gate);
+  g.b0 = static_cast<const u16*>(b_gate);
+  g.w1 = w_up;
+  g.s1 = static_cast<const u16*>(s_up);
+  g.b1 = static_cast<const u16*>(b_up);
+  g.y = h;
+  g.ldx = H;
+  g.ldy = I;
+  g.K = (int)H;
+  g.N = (int)I;
+  g.row_div = (int)k;
+  g.P_max = P;
+  if ((st = launch_gather<kSwiGLU>(g, (int)E, bits, s))) return st;
+
+  GatherArgs d{};
+  d.x = h;
+  d.row_index = nullptr;
+  d.offsets = offsets;
+  d.w0 = w_down;
+  d.s0 = static_cast<const u16*>(s_down);
+  d.b0 = static_cast<const u16*>(b_down);
+  d.y = ypair;
+  d.ldx = I;
+  d.ldy = H;
+  d.K = (int)I;
+  d.N = (int)H;
+  d.row_div = 1;
+  d.P_max = P;
+  if ((st = launch_gather<kPlain>(d, (int)E, bits, s))) return st;
+
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)M, (unsigned)((H + 255) / 256)), dim3(256), 0, s, ypair, pos,
+                     scores_ws, static_cast<u16*>(out), (int)H, (int)k);
+  return check_launch("moe combine");
+}

@@ -1,0 +1,232 @@
+// Dense small-M affine qmm, split-K across workgroups (gfx950).
+//
+// Workgroup = NS waves = NS tiles of 16 output features ("strip" of 16*NS rows) x one slice of
+// K (blockIdx.y). The slice of x (16 rows x slice) is staged once in LDS and shared by the NS
+// waves, together with its per-group row sums (the bias term's sum_j x[m, j], reduced across
+// 8 lanes during staging). Each wave issues every weight load of its 16 rows x slice up front
+// (one 16/8-byte load per row-group per lane, straight from the packed row), loads scales and
+// biases 8 groups per 16-byte load, then runs the MFMA loop reading x fragments from LDS.
+// Slices of one strip are combined by the last workgroup to finish (a device-scope arrival
+// counter per strip), always in slice order 0..S-1, so the result is deterministic and
+// independent of M and of arrival order.
+#pragma once
+
+#include "dspark_qmm_core.h"
+
+namespace dspark {
+
+constexpr int kQmmMaxProblems = DSPARK_QMM_MAX_PROBLEMS;
+constexpr int kQmmMaxSlices = 16;
+
+struct QmmSkProb {
+  const u16* x;
+  const u32* w;
+  const u16* s;
+  const u16* b;
+  u16* y;
+  float* part;  // [mtiles][strips][S][16][16*NS] fp32 partials (S > 1)
+  int* ctr;     // [mtiles][strips] arrival counters (zero between calls)
+  long ldx;
+  long ldy;
+  int N;
+  int K;
+  int strip0;  // first blockIdx.x of this problem
+  int strips;
+};
+
+struct QmmSkArgs {
+  QmmSkProb p[kQmmMaxProblems];
+  int count;
+  int M;
+  int S;  // K slices (<= kQmmMaxSlices)
+};
+
+__device__ __forceinline__ u32x4_t lds128(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+// bf16 field `i` (0..7) of a 16-byte vector of 8 bf16
+__device__ __forceinline__ u32 bf_field(u32x4_t v, int i) {
+  const u32 wd = v[i >> 1];
+  return (i & 1) ? (wd >> 16) : (wd & 0xFFFFu);
+}
+
+__device__ __forceinline__ float sum_bf16x8(u32x4_t v) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s += bf2f(v[i] & 0xFFFFu) + bf2f(v[i] >> 16);
+  return s;
+}
+
+template <int BITS, int NS, int KSMAX, bool SBVEC>
+__global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
+  constexpr int XP = KSMAX * 64 + 8;  // LDS row pitch of the staged x slice (elements)
+  __shared__ __attribute__((aligned(16))) u16 xs[16 * XP];
+  // per group: 16 row sums (8-bit: sum x; 4-bit: -128 * sum x, the MFMA seed)
+  __shared__ __attribute__((aligned(16))) float xsum[KSMAX * 16];
+  __shared__ int last_flag;
+
+  const int bx = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kQmmMaxProblems; ++i)
+    if (i < args.count && bx >= args.p[i].strip0) pi = i;
+  const QmmSkProb& P = args.p[pi];
+  const int N = P.N, K = P.K;
+  const int strip = bx - P.strip0;
+  const int S = args.S;
+  const int sl = blockIdx.y;
+  const int mt = blockIdx.z;
+  const int G = K >> 6;
+  const int gs = (sl * G) / S, ge = ((sl + 1) * G) / S, gcount = ge - gs;
+  const int m_base = mt * 16;
+  const int m_rows = min(16, args.M - m_base);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int ncol = strip * 16 * NS + 16 * wave + c16;
+  const int n = min(ncol, N - 1);
+
+  // ---- 1. every weight fragment of this lane's row in the slice (clamped, unconditional)
+  WFrag<BITS> wf[KSMAX];
+  const u32* wr = wrow_ptr<BITS>(P.w, n, K, q);
+#pragma unroll
+  for (int gl = 0; gl < KSMAX; ++gl) {
+    const int g = gs + min(gl, gcount - 1);
+    if constexpr (BITS == 4)
+      wf[gl].v = ldg64(wr + 8 * g);
+    else
+      wf[gl].v = ldg128(wr + 16 * g);
+  }
+  // ---- 2. scales / biases of the row's groups in the slice
+  constexpr int SBV = (KSMAX + 7) / 8;
+  u32x4_t svv[SBV], bvv[SBV];
+  u32 svs[SBVEC ? 1 : KSMAX], bvs[SBVEC ? 1 : KSMAX];
+  const u16* srow = P.s + (long)n * G + gs;
+  const u16* brow = P.b + (long)n * G + gs;
+  if constexpr (SBVEC) {
+    // gcount is a multiple of 8 and the row/slice starts are 16-byte aligned
+#pragma unroll
+    for (int j = 0; j < SBV; ++j) {
+      const int jj = min(j, (gcount >> 3) - 1);
+      svv[j] = ldg128(srow + 8 * jj);
+      bvv[j] = ldg128(brow + 8 * jj);
+    }
+  } else {
+#pragma unroll
+    for (int gl = 0; gl < KSMAX; ++gl) {
+      const int g = min(gl, gcount - 1);
+      svs[gl] = srow[g];
+      bvs[gl] = brow[g];
+    }
+  }
+  // ---- 3. the x slice (16 rows; rows >= M are clamped duplicates) -> LDS, with group sums.
+  // 16-byte chunk c covers row c / (8*gcount), group (c / 8) % gcount, eighth c % 8; the 8
+  // chunks of one (row, group) sit in 8 consecutive lanes and are summed with xor-shuffles.
+  {
+    const int cpr = gcount * 8;  // chunks per row
+    const int total = 16 * cpr;  // multiple of 64: every wave runs whole iterations
+    const u16* xb = P.x + (long)gs * 64;
+    for (int c = tid; c < total; c += 64 * NS) {
+      const int row = c / cpr, col = c - row * cpr;
+      const int src = m_base + min(row, m_rows - 1);
+      u32x4_t v = ldg128(xb + (long)src * P.ldx + 8 * col);
+      float s8 = sum_bf16x8(v);
+      s8 += shfl_xor(s8, 1);
+      s8 += shfl_xor(s8, 2);
+      s8 += shfl_xor(s8, 4);
+      if (BITS == 4) {
+        // store the 8 values in the (t, t+4) order unpack_u4 produces
+        v = perm_x_u4(v);
+        s8 *= -128.0f;
+      }
+      *reinterpret_cast<u32x4_t*>(&xs[row * XP + 8 * col]) = v;
+      if ((c & 7) == 0) xsum[(col >> 3) * 16 + row] = s8;
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. MFMA loop over the slice
+  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc = zero;
+  const u16* xl = &xs[c16 * XP + 16 * q];
+#pragma unroll
+  for (int gl = 0; gl < KSMAX; ++gl) {
+    if (gl < gcount) {
+      const u32x4_t a0 = lds128(xl + 64 * gl), a1 = lds128(xl + 64 * gl + 8);
+      const u32x4_t cb = lds128(&xsum[gl * 16 + 4 * q]);  // rows 4q..4q+3
+      const f32x4_t c = {__builtin_bit_cast(float, cb.x), __builtin_bit_cast(float, cb.y),
+                         __builtin_bit_cast(float, cb.z), __builtin_bit_cast(float, cb.w)};
+      f32x4_t p;
+      if constexpr (BITS == 4) {
+        p = mfma16x16x32(a0, unpack_u4(wf[gl].v.x), c);  // seeded with -128 * sum x
+        p = mfma16x16x32(a1, unpack_u4(wf[gl].v.y), p);
+      } else {
+        p = mfma16x16x32(a0, unpack_u8(wf[gl].v.x, wf[gl].v.y), zero);
+        p = mfma16x16x32(a1, unpack_u8(wf[gl].v.z, wf[gl].v.w), p);
+      }
+      u32 sbits, bbits;
+      if constexpr (SBVEC) {
+        sbits = bf_field(svv[gl >> 3], gl & 7);
+        bbits = bf_field(bvv[gl >> 3], gl & 7);
+      } else {
+        sbits = svs[gl];
+        bbits = bvs[gl];
+      }
+      const float sf = bf2f(sbits), bf = bf2f(bbits) * bias_mul;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bf, c[r], __builtin_fmaf(sf, p[r], acc[r]));
+    }
+  }
+
+  // ---- 5. epilogue: lane holds y[m_base + 4q + r][ncol]
+  if (S == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * q + r;
+      if (m < m_rows && ncol < N) P.y[(long)(m_base + m) * P.ldy + ncol] = f2bf(acc[r]);
+    }
+    return;
+  }
+  // Partials travel through device-coherent (sc1) stores and loads, so no L2 write-back or
+  // invalidate is needed: each thread waits for its stores to complete before the workgroup
+  // arrives on the strip's counter (device-scope atomic), and the last arriver reads the other
+  // slices with coherent loads, summing in slice order.
+  constexpr int TW = 16 * NS;  // strip width
+  const long tile = (long)mt * P.strips + strip;
+  float* part = P.part + (tile * S) * (16 * TW);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    __hip_atomic_store(&part[(long)sl * (16 * TW) + (4 * q + r) * TW + 16 * wave + c16], acc[r], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this thread's partial stores are complete
+  __syncthreads();
+  if (tid == 0)
+    last_flag = (__hip_atomic_fetch_add(&P.ctr[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1);
+  __syncthreads();
+  if (!last_flag) return;
+  // 16*TW outputs, 4 per thread; all S partials of all 4 are requested before summing
+  float pv[4][kQmmMaxSlices];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + i * 64 * NS;
+#pragma unroll
+    for (int s2 = 0; s2 < kQmmMaxSlices; ++s2)
+      pv[i][s2] = __hip_atomic_load(&part[(long)min(s2, S - 1) * (16 * TW) + e], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + i * 64 * NS;
+    const int m = e / TW, col = e - m * TW;
+    float v = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < kQmmMaxSlices; ++s2)
+      if (s2 < S) v += pv[i][s2];
+    const int nc = strip * TW + col;
+    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v);
+  }
+  if (tid == 0) __hip_atomic_store(&P.ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace dspark

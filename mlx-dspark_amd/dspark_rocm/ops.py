@@ -1,0 +1,270 @@
+"""Torch-facing wrappers of the C ABI: tensor checks, output allocation, current HIP stream.
+
+These are the product path: every function here launches a hand-written gfx950 kernel through
+``libdspark_rocm.so`` and raises if the library is unavailable or the call is refused.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+GROUP = 64
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("dspark kernels need tensors on a ROCm device (cuda:N)")
+
+
+def _require_bf16(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name}: expected bfloat16, got {t.dtype}")
+
+
+def _require_packed(w: torch.Tensor) -> None:
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed weights must be int32/uint32 words, got {w.dtype}")
+
+
+def _rowmajor(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 2 or t.stride(-1) != 1:
+        raise ValueError(f"{name}: expected a 2-D tensor with unit stride along the last dim")
+
+
+# ---------------------------------------------------------------------------- quantized matmul
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                     *, group_size: int = GROUP, bits: int = 4, out: torch.Tensor | None = None
+                     ) -> torch.Tensor:
+    """``x [..., K] @ dequant(w)^T -> [..., N]`` (bf16) on the gfx950 qmm kernel.
+
+    ``w`` packed [N, K*bits/32], ``scales``/``biases`` bf16 [N, K/64]. Any number of rows
+    (served in 16-row tiles); the small-M shapes of speculative verify are the target.
+    Mirrors ``mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)``.
+    """
+    _require_cuda(x, w, scales, biases)
+    _require_bf16("x", x)
+    _require_packed(w)
+    _require_bf16("scales", scales)
+    _require_bf16("biases", biases)
+    k = x.shape[-1]
+    n = w.shape[0]
+    if w.shape[1] * 32 // bits != k:
+        raise ValueError(f"x K={k} does not match packed weight {tuple(w.shape)} at {bits} bits")
+    if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
+        raise ValueError(f"scales/biases must be [{n}, {k // group_size}]")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    w = w.contiguous()
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    else:
+        _rowmajor("out", out)
+        if out.shape != (m, n) or out.dtype != torch.bfloat16:
+            raise ValueError(f"out must be bf16 [{m}, {n}]")
+    if m:
+        _lib.call("dspark_qmm_affine", _ptr(x2), x2.stride(0), m, k, _ptr(w), _ptr(scales),
+                  _ptr(biases), n, bits, group_size, _ptr(out), out.stride(0), _stream(x))
+    return out.reshape(*lead, n)
+
+
+def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = GROUP, bits: int = 4,
+                           outs=None) -> list[torch.Tensor]:
+    """Several ``quantized_matmul`` with the same M, K and bits in ONE launch (q/k/v; gate/up).
+    Bitwise equal to separate calls."""
+    cnt = len(w_list)
+    if not 1 <= cnt <= _lib.MAX_QMM_PROBLEMS:
+        raise ValueError(f"1..{_lib.MAX_QMM_PROBLEMS} problems per launch, got {cnt}")
+    if len(x_list) == 1 and cnt > 1:
+        x_list = list(x_list) * cnt
+    probs = (_lib.QmmProblem * cnt)()
+    results = []
+    m = None
+    keep = []
+    for i in range(cnt):
+        x, w, s, b = x_list[i], w_list[i], s_list[i], b_list[i]
+        _require_cuda(x, w, s, b)
+        _require_bf16("x", x)
+        _require_packed(w)
+        k = x.shape[-1]
+        x2 = x.reshape(-1, k)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        if m is None:
+            m = x2.shape[0]
+        elif x2.shape[0] != m:
+            raise ValueError("all problems must have the same number of rows")
+        n = w.shape[0]
+        w, s, b = w.contiguous(), s.contiguous(), b.contiguous()
+        y = outs[i] if outs is not None else torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+        keep += [x2, w, s, b, y]
+        probs[i] = _lib.QmmProblem(_ptr(x2), x2.stride(0), _ptr(w), _ptr(s), _ptr(b), _ptr(y), y.stride(0), n, k)
+        results.append(y.reshape(*x.shape[:-1], n))
+    _lib.call("dspark_qmm_affine_multi", probs, cnt, m, bits, group_size, _stream(x_list[0]))
+    return results
+
+
+def qmm_supported(m: int, k: int, n: int, bits: int, group_size: int = GROUP) -> bool:
+    return _lib.load().dspark_qmm_affine_supported(m, k, n, bits, group_size) == 0
+
+
+# ---------------------------------------------------------------------------- workspaces
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A per-(device, stream) scratch buffer reused across calls (stream-ordered reuse is safe;
+    two streams never share one). Grows, never shrinks."""
+    if nbytes <= 0:
+        return None
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _workspaces[key] = buf
+    return buf
+
+
+# ---------------------------------------------------------------------------- verify attention
+
+ATTN_HEAD_DIMS = (64, 128)
+
+
+def _i64x3(t: torch.Tensor):
+    arr = (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+    return arr
+
+
+def verify_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, causal: bool = True,
+                     tree_anc: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``softmax(scale * q k^T + mask) v`` for few verify rows over a (strided) KV cache view.
+
+    q bf16 [B, Hq, Mq, D]; k/v bf16 [B, Hk, L, D] with unit stride along D (any batch/head/seq
+    strides, e.g. a ``[..., :L, :]`` slice of a larger cache). ``causal``: row i sees keys
+    ``0 .. L - Mq + i``. ``tree_anc`` (uint32/int32 [Mq]) selects the tree-verify mask.
+    """
+    _require_cuda(q, k, v)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_bf16(name, t)
+        if t.dim() != 4:
+            raise ValueError(f"{name}: expected [B, H, L, D]")
+    B, Hq, mq, D = q.shape
+    Hk, L = k.shape[1], k.shape[2]
+    if k.shape != (B, Hk, L, D) or v.shape != (B, Hk, L, D):
+        raise ValueError(f"k/v must be [{B}, Hk, L, {D}]; got {tuple(k.shape)} / {tuple(v.shape)}")
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("k/v must be contiguous along head_dim")
+    q = q.contiguous()
+    lib = _lib.load()
+    if out is None:
+        out = torch.empty_like(q)
+    nbytes = lib.dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
+    ws = workspace(q.device, nbytes)
+    anc = None
+    if tree_anc is not None:
+        anc = tree_anc.to(device=q.device, dtype=torch.int32).contiguous()
+    _lib.call("dspark_verify_attention", _ptr(q), B, Hq, mq, D, _ptr(k), _ptr(v), _i64x3(k), _i64x3(v), Hk, L,
+              float(scale), int(bool(causal)), _ptr(anc), _ptr(out), _ptr(ws), 0 if ws is None else ws.numel(),
+              _stream(q))
+    return out
+
+
+def verify_attention_blocks(B: int, Hq: int, Hk: int, mq: int, D: int, L: int) -> int:
+    return int(_lib.load().dspark_verify_attention_blocks(B, Hq, Hk, mq, D, L))
+
+
+# ---------------------------------------------------------------------------- MoE
+
+def moe_route(logits: torch.Tensor, k: int, *, renorm: bool = True, bucket: bool = False):
+    """Softmax top-k routing on the GPU. logits bf16 [M, E] -> (inds int32 [M, k], scores bf16
+    [M, k]) and, with ``bucket=True``, also (expert_offsets [E+1], sorted_pairs [M*k],
+    pair_pos [M*k]) of the (token, slot) pairs sorted by expert."""
+    _require_cuda(logits)
+    _require_bf16("logits", logits)
+    logits = logits.contiguous()
+    M, E = logits.shape
+    dev = logits.device
+    inds = torch.empty((M, k), dtype=torch.int32, device=dev)
+    scores = torch.empty((M, k), dtype=torch.bfloat16, device=dev)
+    off = srt = pos = None
+    if bucket:
+        off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        srt = torch.empty(M * k, dtype=torch.int32, device=dev)
+        pos = torch.empty(M * k, dtype=torch.int32, device=dev)
+    _lib.call("dspark_moe_route_topk", _ptr(logits), M, E, k, int(bool(renorm)), _ptr(inds), _ptr(scores),
+              _ptr(off), _ptr(srt), _ptr(pos), _stream(logits))
+    if bucket:
+        return inds, scores, off, srt, pos
+    return inds, scores
+
+
+def gather_qmm_sorted(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                      expert_offsets: torch.Tensor, *, row_index: torch.Tensor | None = None, bits: int = 4,
+                      group_size: int = GROUP, rows: int | None = None) -> torch.Tensor:
+    """Grouped qmm over expert-sorted rows: ``y[p] = x[row_index[p]] @ dequant(w[e])^T`` for
+    ``expert_offsets[e] <= p < expert_offsets[e+1]``. w packed [E, N, K*bits/32]."""
+    _require_cuda(x, w, scales, biases, expert_offsets)
+    _require_bf16("x", x)
+    _require_packed(w)
+    E, N = w.shape[0], w.shape[1]
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    P = rows if rows is not None else (row_index.numel() if row_index is not None else x2.shape[0])
+    y = torch.empty((P, N), dtype=torch.bfloat16, device=x.device)
+    ri = None if row_index is None else row_index.to(torch.int32).contiguous()
+    _lib.call("dspark_gather_qmm", _ptr(x2), x2.stride(0), K, _ptr(ri), _ptr(expert_offsets.to(torch.int32).contiguous()),
+              E, P, _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()), N, bits, group_size,
+              _ptr(y), y.stride(0), _stream(x))
+    return y
+
+
+def moe_switch_glu(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, bits: int = 4,
+                   renorm: bool = True, group_size: int = GROUP):
+    """Routed-expert SwiGLU MLP of one MoE block: route -> gate/up (fused SwiGLU) -> down ->
+    score-weighted combine, four launches. ``gate``/``up``/``down`` are (w, scales, biases) with
+    w packed [E, rows, cols*bits/32]. Returns (out bf16 [M, H], inds [M, k], scores [M, k])."""
+    _require_cuda(x, logits)
+    _require_bf16("x", x)
+    _require_bf16("logits", logits)
+    x = x.contiguous()
+    logits = logits.contiguous()
+    M, H = x.shape
+    E = logits.shape[1]
+    I = gate[0].shape[1]
+    lib = _lib.load()
+    nbytes = lib.dspark_moe_workspace(M, H, I, E, k)
+    if nbytes == 0:
+        raise ValueError(f"unsupported MoE shape M={M} E={E} k={k}")
+    ws = workspace(x.device, nbytes)
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+    inds = torch.empty((M, k), dtype=torch.int32, device=x.device)
+    scores = torch.empty((M, k), dtype=torch.bfloat16, device=x.device)
+    (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
+    _lib.call("dspark_moe_switch_glu", _ptr(x), _ptr(logits), M, H, I, E, k, int(bool(renorm)),
+              _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu), _ptr(su), _ptr(bu), _ptr(wd), _ptr(sd), _ptr(bd),
+              bits, group_size, _ptr(out), _ptr(inds), _ptr(scores), _ptr(ws), ws.numel(), _stream(x))
+    return out, inds, scores

@@ -1,0 +1,58 @@
+"""CPU: the C-ABI library loads and exports every entry point include/dspark.h declares.
+No kernel is launched (there may be no GPU); only the pure shape queries are called."""
+
+from __future__ import annotations
+
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions() -> set[str]:
+    text = open(os.path.join(ROOT, "include", "dspark.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(dspark_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_and_binding_table_agree():
+    from dspark_rocm import _lib
+
+    assert _header_functions() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    from dspark_rocm import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libdspark_rocm.so is not built (run mlx-dspark_amd/build.py)")
+    assert set(_lib.exported_symbols()) == _header_functions()
+    lib = _lib.load()
+    assert b"gfx950" in lib.dspark_version()
+
+
+def test_shape_queries_without_gpu():
+    from dspark_rocm import _lib
+
+    lib = _lib.load()
+    assert lib.dspark_qmm_affine_supported(16, 4096, 4096, 4, 64) == 0
+    assert lib.dspark_qmm_affine_supported(16, 4096, 4096, 3, 64) == -6
+    assert lib.dspark_qmm_affine_supported(16, 4000, 4096, 4, 64) == -2
+    assert lib.dspark_verify_attention_workspace(1, 32, 8, 16, 128, 32784) > 0
+    assert lib.dspark_verify_attention_blocks(1, 32, 8, 16, 128, 32784) > 1
+    assert lib.dspark_verify_attention_blocks(1, 32, 8, 16, 96, 1024) == -1   # unsupported head_dim
+    assert lib.dspark_moe_workspace(16, 2048, 768, 128, 8) > 0
+    assert lib.dspark_moe_workspace(16, 2048, 768, 128, 64) == 0              # k > 32
+    assert lib.dspark_last_error() is not None
+
+
+def test_plan_blocks_scale_with_length():
+    from dspark_rocm import _lib
+
+    lib = _lib.load()
+    nb = [lib.dspark_verify_attention_blocks(1, 32, 8, 16, 128, L + 16) for L in (512, 4096, 16384, 32768)]
+    assert nb == sorted(nb) and nb[0] >= 1
+    # every block covers whole 64-key tiles and the blocks cover the cache
+    assert lib.dspark_verify_attention_workspace(1, 32, 8, 16, 128, 64) == 0   # one block: no partials

@@ -1,0 +1,99 @@
+"""GPU parity of MoE routing, bucketing, gather_qmm and the fused SwitchGLU block.
+
+Routing indices, bucket offsets and the sorted pair order must be bit-exact against the oracle
+(the order rule is documented in oracle/moe_ref.py); scores within one bf16 ulp; expert outputs
+within 2e-2 * RMS. mlx-lm's own MoE code is not in the reference tree, so the oracle is pinned
+by brute force (tests/test_oracle_moe.py).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _util import assert_rms_close, from_dev_bf16, randn_bf16, rng, to_dev_bf16, to_dev_packed
+from oracle import moe_ref, quant_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _logits_with_ties(r, M, E):
+    x = randn_bf16(r, M, E)
+    # deliberate exact ties (same bf16 logit) inside and across the top-k boundary
+    x[0, 5] = x[0, 9] = x[0, E - 3] = x[0].max()
+    x[1, :16] = 2.0
+    x[2, E // 2:] = x[2].max()
+    x[3, :] = 0.0
+    return x
+
+
+@pytest.mark.parametrize("M,E,k", [(16, 128, 8), (1, 128, 8), (4, 64, 4), (16, 256, 8), (33, 128, 2)])
+def test_route_bit_exact(dev, M, E, k):
+    import torch
+
+    from dspark_rocm import ops
+
+    r = rng(M * 1000 + E + k)
+    x = _logits_with_ties(r, M, E) if M >= 4 else randn_bf16(r, M, E)
+    inds, scores, off, srt, pos = ops.moe_route(to_dev_bf16(x, dev), k, bucket=True)
+    ri, rs = moe_ref.route(x, k)
+    assert np.array_equal(inds.cpu().numpy(), ri)
+    got_s = from_dev_bf16(scores)
+    ulp = np.abs(rs) * 2.0 ** -7
+    assert np.all(np.abs(got_s - rs) <= ulp + 1e-9), np.max(np.abs(got_s - rs))
+    ro, rsrt, rpos = moe_ref.bucket(ri, E)
+    assert np.array_equal(off.cpu().numpy(), ro)
+    assert np.array_equal(srt.cpu().numpy(), rsrt)
+    assert np.array_equal(pos.cpu().numpy(), rpos)
+    assert torch.all(inds >= 0) and torch.all(inds < E)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm(dev, bits):
+    import torch
+
+    from dspark_rocm import ops
+
+    r = rng(20 + bits)
+    E, N, K, P = 8, 96, 256, 40
+    experts = np.sort(r.integers(0, E, size=P)).astype(np.int32)
+    experts[experts == 3] = 4                      # an empty expert
+    experts = np.sort(experts)
+    rows = r.integers(0, 12, size=P).astype(np.int32)
+    x = randn_bf16(r, 12, K)
+    mats = [quant_ref.random_packed(r, N, K, bits) for _ in range(E)]
+    w = np.stack([m[0] for m in mats])
+    s = np.stack([m[1] for m in mats])
+    b = np.stack([m[2] for m in mats])
+    offsets = np.concatenate([[0], np.cumsum(np.bincount(experts, minlength=E))]).astype(np.int32)
+    y = ops.gather_qmm_sorted(to_dev_bf16(x, dev), to_dev_packed(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev),
+                              torch.from_numpy(offsets).to(dev), row_index=torch.from_numpy(rows).to(dev), bits=bits)
+    ref = moe_ref.gather_qmm(x, rows, experts, w, s, b, bits)
+    assert_rms_close(from_dev_bf16(y), ref, 2e-2, "gather_qmm")
+
+
+def _moe_weights(r, E, H, I, bits):
+    def stack(n, k):
+        mats = [quant_ref.random_packed(r, n, k, bits) for _ in range(E)]
+        return tuple(np.stack([m[i] for m in mats]) for i in range(3))
+    return stack(I, H), stack(I, H), stack(H, I)
+
+
+def _dev3(t, dev):
+    return to_dev_packed(t[0], dev), to_dev_bf16(t[1], dev), to_dev_bf16(t[2], dev)
+
+
+@pytest.mark.parametrize("M,E,k,H,I,bits", [(16, 8, 2, 256, 128, 4), (5, 16, 4, 512, 192, 8),
+                                             (16, 128, 8, 2048, 768, 4)])
+def test_switch_glu(dev, M, E, k, H, I, bits):
+    from dspark_rocm import ops
+
+    r = rng(M + E + H)
+    x = randn_bf16(r, M, H)
+    logits = randn_bf16(r, M, E)
+    g, u, d = _moe_weights(r, E, H, I, bits)
+    out, inds, scores = ops.moe_switch_glu(to_dev_bf16(x, dev), to_dev_bf16(logits, dev), _dev3(g, dev),
+                                           _dev3(u, dev), _dev3(d, dev), k=k, bits=bits)
+    ref, ri, rs = moe_ref.switch_glu(x, logits, *g, *u, *d, k=k, bits=bits)
+    assert np.array_equal(inds.cpu().numpy(), ri)
+    assert_rms_close(from_dev_bf16(out), ref, 2e-2, "switch_glu")

@@ -1,0 +1,136 @@
+"""GPU parity of the small-M affine qmm (dspark_qmm_affine / _multi) against the oracle.
+
+Bar: max|Δ| <= 2e-2 * RMS(y) (bf16 out, fp32 accumulate); in practice the kernel lands within
+a couple of bf16 ulps, which the tighter per-element check below pins. Structure mirrors the
+reference's tests/test_small_m_qmm.py: every M of the window at both widths (:59-87), bitwise
+row-count invariance (:107-119), ragged N, the refusal paths, plus the full-size C1 shape.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _util import assert_rms_close, from_dev_bf16, randn_bf16, rng, to_dev_bf16, to_dev_packed
+from oracle import c_oracle, qmm_ref, quant_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(seed, m, k, n, bits, quantized=False):
+    r = rng(seed)
+    x = randn_bf16(r, m, k)
+    if quantized:
+        w32 = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+        w, s, b = quant_ref.quantize(w32, bits)
+    else:
+        w, s, b = quant_ref.random_packed(r, n, k, bits)
+    return x, w, s, b
+
+
+def _run(dev, x, w, s, b, bits):
+    from dspark_rocm import ops
+
+    y = ops.quantized_matmul(to_dev_bf16(x, dev), to_dev_packed(w, dev), to_dev_bf16(s, dev),
+                             to_dev_bf16(b, dev), bits=bits)
+    return from_dev_bf16(y)
+
+
+def _check(got, ref_f64, what):
+    ref = quant_ref.bf16_round(ref_f64.astype(np.float32))
+    assert_rms_close(got, ref, 2e-2, what)
+    # tight: within 2 bf16 ulps of the exact result (+ a floor for values near zero)
+    tol = 2.0 ** -7 * np.abs(ref_f64) + 1e-3 * qmm_ref.rms(ref_f64)
+    bad = np.abs(got - ref_f64) > tol
+    assert not bad.any(), f"{what}: {bad.sum()} elements beyond 2 ulps, worst {np.max(np.abs(got - ref_f64)):.4g}"
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
+def test_window_numerics(dev, bits, m):
+    x, w, s, b = _problem(100 + m, m, 512, 4096, bits, quantized=True)
+    got = _run(dev, x, w, s, b, bits)
+    _check(got, qmm_ref.qmm_f64(x, w, s, b, bits), f"{bits}-bit M={m}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("k,n", [(64, 8), (192, 72), (256, 64), (768, 2048), (2048, 768), (12288, 128)])
+def test_shapes(dev, bits, k, n):
+    x, w, s, b = _problem(7 * k + n, 16, k, n, bits)
+    got = _run(dev, x, w, s, b, bits)
+    _check(got, qmm_ref.qmm_f64(x, w, s, b, bits), f"{bits}-bit {k}x{n}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_rows_are_row_count_invariant(dev, bits):
+    """A row's result does not depend on how many rows ride with it (bitwise)."""
+    x, w, s, b = _problem(5, 16, 1024, 512, bits)
+    full = _run(dev, x, w, s, b, bits)
+    for m in range(1, 16):
+        part = _run(dev, x[:m], w, s, b, bits)
+        assert np.array_equal(full[:m], part), (bits, m)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_more_than_16_rows(dev, bits):
+    x, w, s, b = _problem(11, 37, 512, 256, bits)
+    got = _run(dev, x, w, s, b, bits)
+    _check(got, qmm_ref.qmm_f64(x, w, s, b, bits), "M=37")
+    assert np.array_equal(got[:16], _run(dev, x[:16], w, s, b, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_c1_full_size_against_c_oracle(dev, bits):
+    """C1: M=16, N=K=4096 (the C restatement, fp32 factored like the kernel)."""
+    x, w, s, b = _problem(0, 16, 4096, 4096, bits)
+    got = _run(dev, x, w, s, b, bits)
+    ref = c_oracle.qmm(quant_ref.bf16_bits(x), w, quant_ref.bf16_bits(s), quant_ref.bf16_bits(b), bits)
+    _check(got, ref.astype(np.float64), f"C1 {bits}-bit")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_multi_matches_separate_calls(dev, bits):
+    import torch
+
+    from dspark_rocm import ops
+
+    r = rng(3)
+    x = to_dev_bf16(randn_bf16(r, 16, 1024), dev)
+    mats = [quant_ref.random_packed(r, n, 1024, bits) for n in (512, 128, 128)]
+    ws = [to_dev_packed(w, dev) for w, _, _ in mats]
+    ss = [to_dev_bf16(s, dev) for _, s, _ in mats]
+    bs = [to_dev_bf16(b, dev) for _, _, b in mats]
+    multi = ops.quantized_matmul_multi([x], ws, ss, bs, bits=bits)
+    for i in range(3):
+        single = ops.quantized_matmul(x, ws[i], ss[i], bs[i], bits=bits)
+        assert torch.equal(multi[i], single), i
+
+
+def test_strided_x_rows(dev):
+    """x with a row stride larger than K (a view into a wider buffer)."""
+    import torch
+
+    from dspark_rocm import ops
+
+    x, w, s, b = _problem(9, 8, 512, 128, 4)
+    xb = to_dev_bf16(np.concatenate([x, np.zeros((8, 64), np.float32)], axis=1), dev)[:, :512]
+    y = ops.quantized_matmul(xb, to_dev_packed(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev), bits=4)
+    assert torch.equal(y, ops.quantized_matmul(xb.contiguous(), to_dev_packed(w, dev), to_dev_bf16(s, dev),
+                                               to_dev_bf16(b, dev), bits=4))
+
+
+def test_refusals_raise(dev):
+    import torch
+
+    from dspark_rocm import _lib, ops
+
+    x = torch.zeros((4, 96), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((8, 12), dtype=torch.int32, device=dev)
+    s = torch.zeros((8, 1), dtype=torch.bfloat16, device=dev)
+    with pytest.raises((_lib.DsparkError, ValueError)):
+        ops.quantized_matmul(x, w, s, s, bits=4)          # K = 96 is not a multiple of 64
+    lib = _lib.load()
+    assert lib.dspark_qmm_affine_supported(4, 128, 8, 2, 64) == -6
+    assert lib.dspark_qmm_affine_supported(4, 96, 8, 4, 64) == -2
+    assert lib.dspark_qmm_affine_supported(4, 128, 8, 4, 32) == -6
+    assert lib.dspark_qmm_affine_supported(16, 4096, 4096, 8, 64) == 0
