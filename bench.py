@@ -308,6 +308,8 @@ def main() -> None:
     ap.add_argument("--layers", type=int, default=8, help="distinct layers in the rotated pool")
     ap.add_argument("--quick", action="store_true", help="skip the C1/C3/C4 extras and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (for scaling rocprof byte counters)")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -326,6 +328,15 @@ def main() -> None:
     log(f"device {torch.cuda.get_device_name(dev)}; building C2 pool of {a.layers} layers")
     ls = LayerSet(dev, bits, M, a.layers)
     log(f"C2 pool: {ls.weight_bytes * a.layers / 1e9:.2f} GB weights; step bytes {ls.bytes_per_step}")
+
+    if a.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 268435456 bytes read + written by one copy kernel")
+        del src, dst
 
     for i in range(a.warmup):
         ls.step(i)

@@ -58,7 +58,11 @@ const char* dspark_last_error(void);
  * scales  bf16 [N, K/group_size]
  * biases  bf16 [N, K/group_size]
  * y       bf16 [M, N], row stride ldy
- * bits    4 or 8; group_size 64; K % 64 == 0.
+ * bits    4 or 8; group_size 64; K % 64 == 0, K <= 32768.
+ * workspace  device buffer of at least dspark_qmm_affine_workspace(...) bytes, 256-byte
+ *            aligned, whose first part (arrival counters) is ZERO before the first call that
+ *            uses it; every call leaves it zero again. NULL is allowed when the size is 0.
+ *            Calls sharing one workspace must be ordered on one stream.
  *
  * Replaces skinny_qmm.qmm(x2, weight, scales, biases, bits) (skinny_qmm.py:239-246), i.e. the
  * `dspark_skinny_qmm` Metal kernel (skinny_qmm.py:56-171) and, outside its window, the stock
@@ -69,17 +73,20 @@ const char* dspark_last_error(void);
 int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t K,
                       const uint32_t* w, const void* scales, const void* biases,
                       int64_t N, int bits, int group_size,
-                      void* y, int64_t ldy, dspark_stream stream);
+                      void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                      dspark_stream stream);
+
+/* Workspace bytes dspark_qmm_affine needs for this shape (0 = none). */
+size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, int bits, int group_size);
 
 /* 0 if dspark_qmm_affine accepts this shape, else the dspark_status it would return.
  * Mirrors skinny_qmm.fits (skinny_qmm.py:174-181) without launching. */
 int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int bits, int group_size);
 
-/* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size and M
+/* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size, M and K
  * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,
- * biases and y. Same numerics as separate dspark_qmm_affine calls (bitwise).
- * Replaces the per-projection QuantizedLinear calls of one decoder layer
- * (target.py:208-221 → mlx-lm DecoderLayer), which the reference launches one by one. */
+ * biases and y. Replaces the per-projection QuantizedLinear calls of one decoder layer
+ * (target.py:208-221 -> mlx-lm DecoderLayer), which the reference launches one by one. */
 #define DSPARK_QMM_MAX_PROBLEMS 4
 typedef struct dspark_qmm_problem {
   const void* x;
@@ -94,7 +101,11 @@ typedef struct dspark_qmm_problem {
 } dspark_qmm_problem;
 
 int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int count, int64_t M, int bits,
-                            int group_size, dspark_stream stream);
+                            int group_size, void* workspace, size_t workspace_bytes,
+                            dspark_stream stream);
+
+size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* problems, int count, int64_t M,
+                                         int bits, int group_size);
 
 /* ------------------------------------------------------------------ verify attention */
 

@@ -198,11 +198,20 @@ __global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
         ps += p;
       }
     l = l * alpha + ps;
-    u32x4_t pk[2];
+    // P as a bf16 pair hi + lo (hi = bf16(p), lo = bf16(p - hi)): the P.V product keeps ~16
+    // significant bits of p, so the bf16 output rounding is the only error of note.
+    u32x4_t ph[2], pl[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
-      pk[u] = u32x4_t{pack_bf16x2(s[2 * u][0], s[2 * u][1]), pack_bf16x2(s[2 * u][2], s[2 * u][3]),
-                      pack_bf16x2(s[2 * u + 1][0], s[2 * u + 1][1]), pack_bf16x2(s[2 * u + 1][2], s[2 * u + 1][3])};
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float a0 = s[2 * u + h][2 * i], a1 = s[2 * u + h][2 * i + 1];
+          const u32 hi = pack_bf16x2(a0, a1);
+          ph[u][2 * h + i] = hi;
+          pl[u][2 * h + i] = pack_bf16x2(a0 - bf2f(hi & 0xFFFFu), a1 - bf2f(hi >> 16));
+        }
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
       o[t] *= alpha;
@@ -210,7 +219,8 @@ __global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(&vt_lds[vt_off(d, 32 * u + 8 * q4)]);
-        o[t] = mfma16x16x32(vf, pk[u], o[t]);
+        o[t] = mfma16x16x32(vf, ph[u], o[t]);
+        o[t] = mfma16x16x32(vf, pl[u], o[t]);
       }
     }
   }

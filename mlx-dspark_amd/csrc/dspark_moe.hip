@@ -21,8 +21,7 @@
 namespace dspark {
 namespace {
 
-constexpr int kRouteThreads = 256;
-constexpr int kGatherWaves = 4;
+constexpr int kRouteThreads = 1024;  // one wave per token, 16 tokens at a time
 
 struct RouteArgs {
   const u16* logits;
@@ -47,7 +46,7 @@ __device__ __forceinline__ void argbest(float& v, int& id, float v2, int id2) {
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArgs a) {
   extern __shared__ int lds[];
   int* pair_e = lds;                 // [M*k]
-  int* counts = lds + a.M * a.k;     // [E + 1]
+  int* counts = lds + a.M * a.k;     // [kRouteThreads]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int P = a.M * a.k;
   constexpr int NPL = 16;  // experts per lane (E <= 1024)
@@ -104,30 +103,32 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     }
   }
   if (!a.offsets) return;
-  // ---- bucket the (token, slot) pairs by expert, stable in pair id
-  for (int e = threadIdx.x; e <= a.E; e += kRouteThreads) counts[e] = 0;
+  // ---- bucket the (token, slot) pairs by expert, stable in pair id: thread e walks the pairs
+  // in order twice (count, then place); the bucket starts come from an LDS prefix scan.
   __syncthreads();
-  for (int p = threadIdx.x; p < P; p += kRouteThreads) atomicAdd(&counts[pair_e[p]], 1);
+  const int e = threadIdx.x;
+  int cnt = 0;
+  if (e < a.E)
+    for (int p = 0; p < P; ++p) cnt += (pair_e[p] == e);
+  counts[e] = (e < a.E) ? cnt : 0;  // E <= 1024 == kRouteThreads
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int e = 0; e < a.E; ++e) {
-      const int c = counts[e];
-      counts[e] = run;
-      a.offsets[e] = run;
-      run += c;
-    }
-    counts[a.E] = run;
-    a.offsets[a.E] = run;
+  for (int d = 1; d < kRouteThreads; d <<= 1) {  // inclusive Hillis-Steele scan
+    const int add = (e >= d) ? counts[e - d] : 0;
+    __syncthreads();
+    counts[e] += add;
+    __syncthreads();
   }
-  __syncthreads();
-  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
-    const int e = pair_e[p];
-    int r = 0;
-    for (int p2 = 0; p2 < p; ++p2) r += (pair_e[p2] == e);
-    const int dst = counts[e] + r;
-    if (a.sorted) a.sorted[dst] = p;
-    if (a.pos) a.pos[p] = dst;
+  if (e < a.E) {
+    const int start = counts[e] - cnt;
+    a.offsets[e] = start;
+    if (e == a.E - 1) a.offsets[a.E] = counts[e];
+    int r = start;
+    for (int p = 0; p < P; ++p)
+      if (pair_e[p] == e) {
+        if (a.sorted) a.sorted[r] = p;
+        if (a.pos) a.pos[p] = r;
+        ++r;
+      }
   }
 }
 
@@ -150,14 +151,18 @@ struct GatherArgs {
   int K, N, row_div, P_max;
 };
 
-template <int BITS, int MODE, int CH>
-__global__ __launch_bounds__(64 * kGatherWaves) void gather_qmm_kernel(const GatherArgs a) {
-  constexpr int W = kGatherWaves;
-  constexpr int NT = (MODE == kSwiGLU) ? 2 : 1;
+// One workgroup = one expert x CT tiles of 16 output features (SwiGLU: one tile, for gate and
+// for up), K split over the W waves. Each wave walks its K slice in chunks of KSW groups,
+// issuing the chunk's weight / scale-bias / x loads before its MFMAs; the W partial tiles are
+// summed in LDS in wave order. Workgroups of experts no token selected exit at once. Rows
+// are the expert's bucket, 16 at a time.
+template <int BITS, int MODE, int CT, int KSW, int W>
+__global__ __launch_bounds__(64 * W) void gather_qmm_kernel(const GatherArgs a) {
+  constexpr int NTW = (MODE == kSwiGLU) ? 2 * CT : CT;  // weight tiles per wave
   const int e = blockIdx.x;
   const int p0 = a.offsets[e], p1 = min(a.offsets[e + 1], a.P_max);
   if (p0 >= p1) return;
-  const int n_base = blockIdx.y * 16;
+  const int n_base = blockIdx.y * 16 * CT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c16 = lane & 15, q = lane >> 4;
   const int G = a.K >> 6;
@@ -165,42 +170,101 @@ __global__ __launch_bounds__(64 * kGatherWaves) void gather_qmm_kernel(const Gat
   const long wstride = (long)a.N * (a.K * BITS / 32);
   const long sstride = (long)a.N * G;
 
-  const int n = min(n_base + c16, a.N - 1);
-  const u32* wr[NT];
-  const u16* sr[NT];
-  const u16* br[NT];
-  wr[0] = wrow_ptr<BITS>(a.w0 + e * wstride, n, a.K, q);
-  sr[0] = a.s0 + e * sstride + (long)n * G;
-  br[0] = a.b0 + e * sstride + (long)n * G;
-  if constexpr (MODE == kSwiGLU) {
-    wr[NT - 1] = wrow_ptr<BITS>(a.w1 + e * wstride, n, a.K, q);
-    sr[NT - 1] = a.s1 + e * sstride + (long)n * G;
-    br[NT - 1] = a.b1 + e * sstride + (long)n * G;
+  const u32* wr[NTW];
+  const u16* sr[NTW];
+  const u16* br[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int ct = (MODE == kSwiGLU) ? (j >> 1) : j;
+    const bool up = (MODE == kSwiGLU) && (j & 1);
+    const int n = min(n_base + 16 * ct + c16, a.N - 1);
+    wr[j] = wrow_ptr<BITS>((up ? a.w1 : a.w0) + e * wstride, n, a.K, q);
+    sr[j] = (up ? a.s1 : a.s0) + e * sstride + (long)n * G;
+    br[j] = (up ? a.b1 : a.b0) + e * sstride + (long)n * G;
   }
-  __shared__ float red[W][NT][256];
+  constexpr u32 kconst = (BITS == 4) ? 0xC300C300u : 0x3F803F80u;
+  const u32x4_t kb = {kconst, kconst, kconst, kconst};
+  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  __shared__ float red[W][NTW][256];
   for (int mb = p0; mb < p1; mb += 16) {
-    const int p = min(mb + c16, p1 - 1);
-    const int src = (a.row_index ? a.row_index[p] : p) / a.row_div;
+    const int pr = min(mb + c16, p1 - 1);
+    const int src = (a.row_index ? a.row_index[pr] : pr) / a.row_div;
     const u16* xr = a.x + (long)src * a.ldx + 16 * q;
-    f32x4_t acc[NT];
+    f32x4_t acc[NTW];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    qmm_wave_partial<BITS, NT, CH>(xr, wr, sr, br, g0, g1, acc);
-    __syncthreads();  // previous m-tile's reduction has read red
+    for (int j = 0; j < NTW; ++j) acc[j] = zero;
+    for (int gc = g0; gc < g1; gc += KSW) {
+      const int cnt = min(KSW, g1 - gc);
+      WFrag<BITS> wf[KSW][NTW];
+      u32 sb[KSW][NTW];  // scale (low half) and bias (high half) bf16 bits
+      u32x4_t xa[KSW][2];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+      for (int i = 0; i < KSW; ++i) {
+        const int g = gc + min(i, cnt - 1);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          if constexpr (BITS == 4)
+            wf[i][j].v = ldg64(wr[j] + 8 * g);
+          else
+            wf[i][j].v = ldg128(wr[j] + 16 * g);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < KSW; ++i) {
+        const int g = gc + min(i, cnt - 1);
+        xa[i][0] = ldg128(xr + 64 * g);
+        xa[i][1] = ldg128(xr + 64 * g + 8);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) sb[i][j] = (u32)sr[j][g] | ((u32)br[j][g] << 16);
+      }
+#pragma unroll
+      for (int i = 0; i < KSW; ++i) {
+        if (i < cnt) {
+          u32x4_t a0 = xa[i][0], a1 = xa[i][1];
+          if constexpr (BITS == 4) {
+            a0 = perm_x_u4(a0);
+            a1 = perm_x_u4(a1);
+          }
+          f32x4_t c = mfma16x16x32(a0, kb, zero);
+          c = mfma16x16x32(a1, kb, c);
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            f32x4_t p;
+            if constexpr (BITS == 4) {
+              p = mfma16x16x32(a0, unpack_u4(wf[i][j].v.x), c);
+              p = mfma16x16x32(a1, unpack_u4(wf[i][j].v.y), p);
+            } else {
+              p = mfma16x16x32(a0, unpack_u8(wf[i][j].v.x, wf[i][j].v.y), zero);
+              p = mfma16x16x32(a1, unpack_u8(wf[i][j].v.z, wf[i][j].v.w), p);
+            }
+            const float sf = bf2f(sb[i][j] & 0xFFFFu), bf = bf2f(sb[i][j] >> 16) * bias_mul;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(bf, c[r], __builtin_fmaf(sf, p[r], acc[j][r]));
+          }
+        }
+      }
+    }
+    __syncthreads();  // the previous row tile's reduction has read red
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[wave][j][(4 * q + r) * 16 + c16] = acc[j][r];
     __syncthreads();
-    for (int t = threadIdx.x; t < 256; t += 64 * W) {
-      const int m = t >> 4, nn = t & 15;
+    for (int t = threadIdx.x; t < 256 * CT; t += 64 * W) {
+      const int ct = t >> 8, el = t & 255;
+      const int m = el >> 4, nn = el & 15;
       float v0 = 0.f, v1 = 0.f;
 #pragma unroll
       for (int ww = 0; ww < W; ++ww) {
-        v0 += red[ww][0][t];
-        if constexpr (MODE == kSwiGLU) v1 += red[ww][NT - 1][t];
+        if constexpr (MODE == kSwiGLU) {
+          v0 += red[ww][2 * ct][el];
+          v1 += red[ww][2 * ct + 1][el];
+        } else {
+          v0 += red[ww][ct][el];
+        }
       }
-      const int pp = mb + m, nf = n_base + nn;
+      const int pp = mb + m, nf = n_base + 16 * ct + nn;
       if (pp < p1 && nf < a.N) {
         float out = v0;
         if constexpr (MODE == kSwiGLU) {
@@ -238,18 +302,28 @@ int check_route(long M, long E, long k) {
 }
 
 int launch_route(const RouteArgs& a, hipStream_t s) {
-  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + a.E + 1);
+  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + kRouteThreads);
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), lds, s, a);
   return check_launch("moe_route_topk");
 }
 
+template <int MODE, int W>
+int launch_gather_k(const GatherArgs& a, int E, int bits, hipStream_t s) {
+  constexpr int CT = (MODE == kSwiGLU) ? 1 : 2;  // 16 (gate + up) or 32 output features
+  constexpr int KSW = 4;                         // groups per load chunk
+  const dim3 grid((unsigned)E, (unsigned)((a.N + 16 * CT - 1) / (16 * CT)));
+  if (bits == 4) hipLaunchKernelGGL((gather_qmm_kernel<4, MODE, CT, KSW, W>), grid, dim3(64 * W), 0, s, a);
+  else hipLaunchKernelGGL((gather_qmm_kernel<8, MODE, CT, KSW, W>), grid, dim3(64 * W), 0, s, a);
+  return check_launch(MODE == kSwiGLU ? "moe gate/up" : "gather_qmm");
+}
+
+// K split over W in {4, 8, 16} waves: each wave's slice is about one 4-group load chunk.
 template <int MODE>
 int launch_gather(const GatherArgs& a, int E, int bits, hipStream_t s) {
-  const dim3 grid((unsigned)E, (unsigned)((a.N + 15) / 16));
-  constexpr int CH = 4;
-  if (bits == 4) hipLaunchKernelGGL((gather_qmm_kernel<4, MODE, CH>), grid, dim3(64 * kGatherWaves), 0, s, a);
-  else hipLaunchKernelGGL((gather_qmm_kernel<8, MODE, CH>), grid, dim3(64 * kGatherWaves), 0, s, a);
-  return check_launch(MODE == kSwiGLU ? "moe gate/up" : "gather_qmm");
+  const int G = a.K / 64;
+  if (G <= 16) return launch_gather_k<MODE, 4>(a, E, bits, s);
+  if (G <= 32) return launch_gather_k<MODE, 8>(a, E, bits, s);
+  return launch_gather_k<MODE, 16>(a, E, bits, s);
 }
 
 int check_qmm_format(long K, long N, int bits, int group_size) {

@@ -22,140 +22,65 @@
 //     Integers 0..255 are exact in bf16, so every product is exact in fp32, as in the
 //     reference's pre-scaled masked-field trick.
 //   * sum_{j in g} x[m, j] (the bias term) comes out of the same MFMA in the output layout.
-//   * K is split across the W waves of a workgroup; the W partial 16x16 tiles are summed in
-//     LDS in a fixed wave order, so results are deterministic and independent of M.
-#include "dspark_qmm_core.h"
+//   * a workgroup = 4 waves = a 64-row strip x one slice of K; the x slice and its group sums
+//     are staged once in LDS and shared by the 4 waves (dspark_qmm_splitk.h). Slices of a
+//     strip are summed by the last workgroup to arrive, in slice order: deterministic and
+//     independent of M. The slice count depends only on the strips and K.
+#include "dspark_qmm_splitk.h"
 
 namespace dspark {
 namespace {
 
-constexpr int kMaxProblems = DSPARK_QMM_MAX_PROBLEMS;
+constexpr int kNS = 4;             // waves (16-row output tiles) per workgroup: 64-row strips
+constexpr int kStripRows = 16 * kNS;
+constexpr int kTargetWorkgroups = 512;  // two per CU on 256 CUs
 
-struct QmmProb {
-  const u16* x;
-  const u32* w;
-  const u16* s;
-  const u16* b;
-  u16* y;
-  long ldx;
-  long ldy;
-  int N;
-  int K;
-  int tile0;  // first workgroup (blockIdx.x) of this problem
-  int pad_;
+// Launch plan shared by the workspace query and the launch: S depends only on the strips and
+// K, never on M, so a row's result does not depend on how many rows ride with it.
+struct Plan {
+  int S;       // K slices
+  int ksmax;   // groups per slice the kernel is instantiated for (8, 16 or 32)
+  int strips;  // 64-row strips over all problems
+  int mtiles;
+  size_t ctr_bytes;
+  size_t part_bytes;
 };
 
-struct QmmArgs {
-  QmmProb p[kMaxProblems];
-  int count;
-  int M;
-};
-
-// One workgroup: NT tiles of 16 output features x one 16-row tile of x, K split over W waves.
-template <int BITS, int W, int NT, int CH>
-__global__ __launch_bounds__(64 * W) void qmm_kernel(const QmmArgs args) {
-  // -------- which problem / tile
-  const int bx = blockIdx.x;
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < kMaxProblems; ++i)
-    if (i < args.count && bx >= args.p[i].tile0) pi = i;
-  const QmmProb& P = args.p[pi];
-  const u16* __restrict__ x = P.x;
-  const u32* __restrict__ w = P.w;
-  const u16* __restrict__ sc = P.s;
-  const u16* __restrict__ bi = P.b;
-  u16* __restrict__ y = P.y;
-  const long ldx = P.ldx;
-  const long ldy = P.ldy;
-  const int N = P.N;
-  const int K = P.K;
-  const int tile0 = P.tile0;
-
-  const int G = K >> 6;
-  const int n_base = (bx - tile0) * (16 * NT);
-  const int m_base = blockIdx.y * 16;
-  const int m_rows = min(16, args.M - m_base);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c16 = lane & 15;
-  const int q = lane >> 4;
-  const int g0 = (wave * G) / W;
-  const int g1 = ((wave + 1) * G) / W;
-
-  const u16* xr = x + (long)(m_base + min(c16, m_rows - 1)) * ldx + 16 * q;
-  const u32* wr[NT];
-  const u16* sr[NT];
-  const u16* br[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int n = min(n_base + 16 * j + c16, N - 1);
-    wr[j] = wrow_ptr<BITS>(w, n, K, q);
-    sr[j] = sc + (long)n * G;
-    br[j] = bi + (long)n * G;
+Plan make_plan(const long* Ns, int count, long K, long M) {
+  Plan p{};
+  const long G = K / 64;
+  long strips = 0;
+  for (int i = 0; i < count; ++i) strips += (Ns[i] + kStripRows - 1) / kStripRows;
+  p.strips = (int)strips;
+  p.mtiles = (int)((M + 15) / 16);
+  // 16 groups (1024 k) per slice; 8 when that leaves fewer than kTargetWorkgroups workgroups
+  long s = (G + 15) / 16;
+  if (strips * s < kTargetWorkgroups) s = (G + 7) / 8;
+  if (s > kQmmMaxSlices) s = kQmmMaxSlices;
+  if (s < (G + 31) / 32) s = (G + 31) / 32;  // a slice holds at most 32 groups
+  if (s < 1) s = 1;
+  p.S = (int)s;
+  const long per = (G + s - 1) / s;
+  p.ksmax = per <= 8 ? 8 : per <= 16 ? 16 : 32;
+  if (p.S > 1) {
+    const size_t ctrs = (size_t)strips * p.mtiles;
+    p.ctr_bytes = ((ctrs * sizeof(int)) + 255) & ~size_t(255);
+    p.part_bytes = ctrs * p.S * 16 * kStripRows * sizeof(float);
   }
-  f32x4_t acc[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  qmm_wave_partial<BITS, NT, CH>(xr, wr, sr, br, g0, g1, acc);
-
-  // -------- split-K reduction over the W waves (fixed order)
-  __shared__ float red[W][NT][256];
-#pragma unroll
-  for (int j = 0; j < NT; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][j][(4 * q + r) * 16 + c16] = acc[j][r];
-  __syncthreads();
-  for (int t = threadIdx.x; t < NT * 256; t += 64 * W) {
-    const int j = t >> 8, e = t & 255;
-    const int m = e >> 4, nn = e & 15;
-    float v = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < W; ++ww) v += red[ww][j][e];
-    const int n = n_base + 16 * j + nn;
-    if (m < m_rows && n < N) y[(long)(m_base + m) * ldy + n] = f2bf(v);
-  }
+  return p;
 }
 
-template <int BITS, int W, int NT, int CH>
-int launch(const QmmArgs& a, int tiles, int mtiles, hipStream_t st) {
-  hipLaunchKernelGGL((qmm_kernel<BITS, W, NT, CH>), dim3(tiles, mtiles, 1), dim3(64 * W, 1, 1), 0, st, a);
+template <int BITS, int KSMAX, bool SBVEC>
+int launch(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
+  hipLaunchKernelGGL((qmm_sk_kernel<BITS, kNS, KSMAX, SBVEC>), dim3(p.strips, p.S, p.mtiles), dim3(64 * kNS), 0, st, a);
   return check_launch("dspark_qmm_affine");
 }
 
-// Launch geometry: workgroups of W waves split K; NT output tiles per workgroup. NT > 1 only
-// when there are enough tiles to keep >= 2 workgroups per CU (256 CUs) busy.
-struct Geometry {
-  int W;
-  int NT;
-};
-
-Geometry choose_geometry(long total_rows, long K) {
-  Geometry g{8, 1};
-  const long G = K / 64;
-  if (G < 16) g.W = 4;
-  if (total_rows >= 16L * 2 * 512) g.NT = 2;
-  return g;
-}
-
-int qmm_dispatch(const QmmArgs& a, int bits, long total_rows, long K, hipStream_t st) {
-  const Geometry geo = choose_geometry(total_rows, K);
-  int tiles = 0;
-  QmmArgs args = a;
-  for (int i = 0; i < a.count; ++i) {
-    args.p[i].tile0 = tiles;
-    tiles += (int)((a.p[i].N + 16 * geo.NT - 1) / (16 * geo.NT));
-  }
-  for (int i = a.count; i < kMaxProblems; ++i) args.p[i] = args.p[0], args.p[i].tile0 = 1 << 30;
-  const int mtiles = (a.M + 15) / 16;
-  constexpr int CH = 4;
-  if (bits == 4) {
-    if (geo.W == 8) return geo.NT == 2 ? launch<4, 8, 2, CH>(args, tiles, mtiles, st) : launch<4, 8, 1, CH>(args, tiles, mtiles, st);
-    return geo.NT == 2 ? launch<4, 4, 2, CH>(args, tiles, mtiles, st) : launch<4, 4, 1, CH>(args, tiles, mtiles, st);
-  }
-  if (geo.W == 8) return geo.NT == 2 ? launch<8, 8, 2, CH>(args, tiles, mtiles, st) : launch<8, 8, 1, CH>(args, tiles, mtiles, st);
-  return geo.NT == 2 ? launch<8, 4, 2, CH>(args, tiles, mtiles, st) : launch<8, 4, 1, CH>(args, tiles, mtiles, st);
+template <int BITS>
+int launch_bits(const QmmSkArgs& a, const Plan& p, bool sbvec, hipStream_t st) {
+  if (p.ksmax == 8) return sbvec ? launch<BITS, 8, true>(a, p, st) : launch<BITS, 8, false>(a, p, st);
+  if (p.ksmax == 16) return sbvec ? launch<BITS, 16, true>(a, p, st) : launch<BITS, 16, false>(a, p, st);
+  return sbvec ? launch<BITS, 32, true>(a, p, st) : launch<BITS, 32, false>(a, p, st);
 }
 
 int check_common(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
@@ -163,19 +88,35 @@ int check_common(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
   if (group_size != 64) return fail(DSPARK_ERR_UNSUPPORTED, "qmm: group_size=%d (64 supported)", group_size);
   if (M < 1 || N < 1 || K < 64) return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   if (K % 64) return fail(DSPARK_ERR_SHAPE, "qmm: K=%lld is not a multiple of 64", (long long)K);
-  if (M > (1 << 20) || N > (1L << 30) / 16 || K > (1L << 24))
-    return fail(DSPARK_ERR_SHAPE, "qmm: shape too large (M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+  if (K > 32 * 16 * 64) return fail(DSPARK_ERR_SHAPE, "qmm: K=%lld > 32768", (long long)K);
+  if (M > (1 << 20) || N > (1L << 30) / 16)
+    return fail(DSPARK_ERR_SHAPE, "qmm: shape too large (M=%lld N=%lld)", (long long)M, (long long)N);
   return DSPARK_OK;
 }
 
-int check_problem(const dspark_qmm_problem& p, int64_t M, int bits) {
+int check_problem(const dspark_qmm_problem& p) {
   if (!p.x || !p.w || !p.scales || !p.biases || !p.y) return fail(DSPARK_ERR_ARG, "qmm: null pointer");
-  if (!aligned(p.x, 16) || (p.ldx % 8) != 0) return fail(DSPARK_ERR_ALIGN, "qmm: x must be 16-byte aligned with ldx %% 8 == 0 (ldx=%lld)", (long long)p.ldx);
+  if (!aligned(p.x, 16) || (p.ldx % 8) != 0)
+    return fail(DSPARK_ERR_ALIGN, "qmm: x must be 16-byte aligned with ldx %% 8 == 0 (ldx=%lld)", (long long)p.ldx);
   if (!aligned(p.w, 16)) return fail(DSPARK_ERR_ALIGN, "qmm: packed weights must be 16-byte aligned");
-  if (!aligned(p.scales, 2) || !aligned(p.biases, 2) || !aligned(p.y, 2)) return fail(DSPARK_ERR_ALIGN, "qmm: bf16 buffers must be 2-byte aligned");
-  if (p.ldx < p.K || p.ldy < p.N) return fail(DSPARK_ERR_SHAPE, "qmm: ldx=%lld < K=%lld or ldy=%lld < N=%lld", (long long)p.ldx, (long long)p.K, (long long)p.ldy, (long long)p.N);
-  (void)M;
-  (void)bits;
+  if (!aligned(p.scales, 2) || !aligned(p.biases, 2) || !aligned(p.y, 2))
+    return fail(DSPARK_ERR_ALIGN, "qmm: bf16 buffers must be 2-byte aligned");
+  if (p.ldx < p.K || p.ldy < p.N)
+    return fail(DSPARK_ERR_SHAPE, "qmm: ldx=%lld < K=%lld or ldy=%lld < N=%lld", (long long)p.ldx, (long long)p.K,
+                (long long)p.ldy, (long long)p.N);
+  return DSPARK_OK;
+}
+
+int validate(const dspark_qmm_problem* problems, int count, int64_t M, int bits, int group_size, long* Ns) {
+  if (!problems || count < 1 || count > kQmmMaxProblems)
+    return fail(DSPARK_ERR_ARG, "qmm: problem count %d (1..%d)", count, kQmmMaxProblems);
+  for (int i = 0; i < count; ++i) {
+    int st = check_common(M, problems[i].K, problems[i].N, bits, group_size);
+    if (st) return st;
+    if ((st = check_problem(problems[i]))) return st;
+    if (problems[i].K != problems[0].K) return fail(DSPARK_ERR_SHAPE, "qmm: all problems of one launch must share K");
+    Ns[i] = problems[i].N;
+  }
   return DSPARK_OK;
 }
 
@@ -188,39 +129,76 @@ extern "C" int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int 
   return check_common(M, K, N, bits, group_size);
 }
 
+extern "C" size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* problems, int count, int64_t M,
+                                                    int bits, int group_size) {
+  long Ns[kQmmMaxProblems];
+  if (validate(problems, count, M, bits, group_size, Ns)) return 0;
+  const Plan p = make_plan(Ns, count, problems[0].K, M);
+  return p.ctr_bytes + p.part_bytes;
+}
+
+extern "C" size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
+  if (check_common(M, K, N, bits, group_size)) return 0;
+  long Ns[1] = {(long)N};
+  const Plan p = make_plan(Ns, 1, K, M);
+  return p.ctr_bytes + p.part_bytes;
+}
+
 extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int count, int64_t M, int bits,
-                                       int group_size, dspark_stream stream) {
-  if (!problems || count < 1 || count > kMaxProblems)
-    return fail(DSPARK_ERR_ARG, "qmm_multi: count=%d (1..%d)", count, kMaxProblems);
-  QmmArgs a{};
+                                       int group_size, void* workspace, size_t workspace_bytes,
+                                       dspark_stream stream) {
+  long Ns[kQmmMaxProblems];
+  int st = validate(problems, count, M, bits, group_size, Ns);
+  if (st) return st;
+  const long K = problems[0].K;
+  const Plan p = make_plan(Ns, count, K, M);
+  const size_t need = p.ctr_bytes + p.part_bytes;
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(DSPARK_ERR_WORKSPACE, "qmm: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (need && !aligned(workspace, 256)) return fail(DSPARK_ERR_ALIGN, "qmm: workspace must be 256-byte aligned");
+  const long G = K / 64;
+  bool sbvec = (G % p.S == 0) && ((G / p.S) % 8 == 0);
+  QmmSkArgs a{};
   a.count = count;
   a.M = (int)M;
-  long total_rows = 0, kmax = 0;
+  a.S = p.S;
+  int strip0 = 0;
+  int* ctr = static_cast<int*>(workspace);
+  float* part = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.ctr_bytes) : nullptr;
   for (int i = 0; i < count; ++i) {
-    const dspark_qmm_problem& p = problems[i];
-    int st = check_common(M, p.K, p.N, bits, group_size);
-    if (st) return st;
-    st = check_problem(p, M, bits);
-    if (st) return st;
-    if (p.K != problems[0].K) return fail(DSPARK_ERR_SHAPE, "qmm_multi: all problems must share K");
-    a.p[i].x = static_cast<const u16*>(p.x);
-    a.p[i].w = p.w;
-    a.p[i].s = static_cast<const u16*>(p.scales);
-    a.p[i].b = static_cast<const u16*>(p.biases);
-    a.p[i].y = static_cast<u16*>(p.y);
-    a.p[i].ldx = p.ldx;
-    a.p[i].ldy = p.ldy;
-    a.p[i].N = (int)p.N;
-    a.p[i].K = (int)p.K;
-    total_rows += p.N;
-    kmax = p.K > kmax ? p.K : kmax;
+    const dspark_qmm_problem& q = problems[i];
+    QmmSkProb& d = a.p[i];
+    d.x = static_cast<const u16*>(q.x);
+    d.w = q.w;
+    d.s = static_cast<const u16*>(q.scales);
+    d.b = static_cast<const u16*>(q.biases);
+    d.y = static_cast<u16*>(q.y);
+    d.ldx = q.ldx;
+    d.ldy = q.ldy;
+    d.N = (int)q.N;
+    d.K = (int)K;
+    d.strips = (int)((q.N + kStripRows - 1) / kStripRows);
+    d.strip0 = strip0;
+    if (need) {
+      d.ctr = ctr;
+      d.part = part;
+      ctr += (size_t)d.strips * p.mtiles;
+      part += (size_t)d.strips * p.mtiles * p.S * 16 * kStripRows;
+    }
+    strip0 += d.strips;
+    sbvec = sbvec && aligned(q.scales, 16) && aligned(q.biases, 16);
   }
-  return qmm_dispatch(a, bits, total_rows, kmax, static_cast<hipStream_t>(stream));
+  for (int i = count; i < kQmmMaxProblems; ++i) {
+    a.p[i] = a.p[0];
+    a.p[i].strip0 = 1 << 30;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return bits == 4 ? launch_bits<4>(a, p, sbvec, s) : launch_bits<8>(a, p, sbvec, s);
 }
 
 extern "C" int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t K, const uint32_t* w,
                                  const void* scales, const void* biases, int64_t N, int bits, int group_size,
-                                 void* y, int64_t ldy, dspark_stream stream) {
+                                 void* y, int64_t ldy, void* workspace, size_t workspace_bytes, dspark_stream stream) {
   dspark_qmm_problem p{x, ldx, w, scales, biases, y, ldy, N, K};
-  return dspark_qmm_affine_multi(&p, 1, M, bits, group_size, stream);
+  return dspark_qmm_affine_multi(&p, 1, M, bits, group_size, workspace, workspace_bytes, stream);
 }

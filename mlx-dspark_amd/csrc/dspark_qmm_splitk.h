@@ -154,9 +154,9 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   for (int gl = 0; gl < KSMAX; ++gl) {
     if (gl < gcount) {
       const u32x4_t a0 = lds128(xl + 64 * gl), a1 = lds128(xl + 64 * gl + 8);
-      const u32x4_t cb = lds128(&xsum[gl * 16 + 4 * q]);  // rows 4q..4q+3
-      const f32x4_t c = {__builtin_bit_cast(float, cb.x), __builtin_bit_cast(float, cb.y),
-                         __builtin_bit_cast(float, cb.z), __builtin_bit_cast(float, cb.w)};
+      // rows 4q..4q+3. (Read as a float vector: bit-casting ext-vector elements one by one
+      // miscompiles to a single-dword read.)
+      const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[gl * 16 + 4 * q]);
       f32x4_t p;
       if constexpr (BITS == 4) {
         p = mfma16x16x32(a0, unpack_u4(wf[gl].v.x), c);  // seeded with -128 * sum x
@@ -227,6 +227,103 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v);
   }
   if (tid == 0) __hip_atomic_store(&P.ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace dspark
+
+namespace dspark {
+
+// Intra-workgroup split-K variant for small N (few 16-row tiles): workgroup = W waves = one
+// 16-row output tile; wave w takes groups [w*G/W, (w+1)*G/W) (at most KSW) and issues all of
+// its weight, x and scale/bias loads up front; the W partial tiles are summed in LDS in wave
+// order. No cross-workgroup exchange, so the critical path is one memory round trip.
+// x fragments come straight from global memory (L2-resident), the group sums of x from an
+// MFMA against a constant operand.
+template <int BITS, int W, int KSW>
+__global__ __launch_bounds__(64 * W) void qmm_ws_kernel(const QmmSkArgs args) {
+  __shared__ float red[W][256];
+  const int bx = blockIdx.x;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kQmmMaxProblems; ++i)
+    if (i < args.count && bx >= args.p[i].strip0) pi = i;
+  const QmmSkProb& P = args.p[pi];
+  const int N = P.N, K = P.K;
+  const int tile = bx - P.strip0;  // 16-row tile
+  const int mt = blockIdx.z;
+  const int G = K >> 6;
+  const int m_base = mt * 16;
+  const int m_rows = min(16, args.M - m_base);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int g0 = (wave * G) / W, g1 = ((wave + 1) * G) / W, gcount = g1 - g0;
+  const int ncol = tile * 16 + c16;
+  const int n = min(ncol, N - 1);
+
+  WFrag<BITS> wf[KSW];
+  u32x4_t xa[KSW][2];
+  u32 sv[KSW], bv[KSW];
+  const u32* wr = wrow_ptr<BITS>(P.w, n, K, q);
+  const u16* xr = P.x + (long)(m_base + min(c16, m_rows - 1)) * P.ldx + 16 * q;
+  const u16* srow = P.s + (long)n * G;
+  const u16* brow = P.b + (long)n * G;
+  if (gcount > 0) {
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int g = g0 + min(i, gcount - 1);
+      if constexpr (BITS == 4)
+        wf[i].v = ldg64(wr + 8 * g);
+      else
+        wf[i].v = ldg128(wr + 16 * g);
+    }
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int g = g0 + min(i, gcount - 1);
+      xa[i][0] = ldg128(xr + 64 * g);
+      xa[i][1] = ldg128(xr + 64 * g + 8);
+      sv[i] = srow[g];
+      bv[i] = brow[g];
+    }
+  }
+  constexpr u32 kconst = (BITS == 4) ? 0xC300C300u : 0x3F803F80u;
+  const u32x4_t kb = {kconst, kconst, kconst, kconst};
+  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc = zero;
+#pragma unroll
+  for (int i = 0; i < KSW; ++i) {
+    if (i < gcount) {
+      u32x4_t a0 = xa[i][0], a1 = xa[i][1];
+      if constexpr (BITS == 4) {
+        a0 = perm_x_u4(a0);
+        a1 = perm_x_u4(a1);
+      }
+      f32x4_t c = mfma16x16x32(a0, kb, zero);
+      c = mfma16x16x32(a1, kb, c);
+      f32x4_t p;
+      if constexpr (BITS == 4) {
+        p = mfma16x16x32(a0, unpack_u4(wf[i].v.x), c);
+        p = mfma16x16x32(a1, unpack_u4(wf[i].v.y), p);
+      } else {
+        p = mfma16x16x32(a0, unpack_u8(wf[i].v.x, wf[i].v.y), zero);
+        p = mfma16x16x32(a1, unpack_u8(wf[i].v.z, wf[i].v.w), p);
+      }
+      const float sf = bf2f(sv[i]), bf = bf2f(bv[i]) * bias_mul;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bf, c[r], __builtin_fmaf(sf, p[r], acc[r]));
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wave][(4 * q + r) * 16 + c16] = acc[r];
+  __syncthreads();
+  if (tid < 256) {
+    float v = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < W; ++ww) v += red[ww][tid];
+    const int m = tid >> 4, nc = tile * 16 + (tid & 15);
+    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v);
+  }
 }
 
 }  // namespace dspark

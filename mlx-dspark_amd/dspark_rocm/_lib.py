@@ -69,9 +69,12 @@ SIGNATURES: dict[str, tuple] = {
     "dspark_version": (c_char_p, []),
     "dspark_last_error": (c_char_p, []),
     "dspark_qmm_affine": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_i64,
-                                  c_int, c_int, c_void_p, c_i64, c_void_p]),
+                                  c_int, c_int, c_void_p, c_i64, c_void_p, c_size_t, c_void_p]),
+    "dspark_qmm_affine_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_int, c_int]),
     "dspark_qmm_affine_supported": (c_int, [c_i64, c_i64, c_i64, c_int, c_int]),
-    "dspark_qmm_affine_multi": (c_int, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int, c_void_p]),
+    "dspark_qmm_affine_multi": (c_int, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int, c_void_p,
+                                        c_size_t, c_void_p]),
+    "dspark_qmm_affine_multi_workspace": (c_size_t, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int]),
     "dspark_verify_attention": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_i64_p,
                                         c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                         c_size_t, c_void_p]),

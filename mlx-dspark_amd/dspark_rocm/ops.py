@@ -82,8 +82,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
         if out.shape != (m, n) or out.dtype != torch.bfloat16:
             raise ValueError(f"out must be bf16 [{m}, {n}]")
     if m:
+        nbytes = _lib.load().dspark_qmm_affine_workspace(m, k, n, bits, group_size)
+        ws = qmm_workspace(x.device, nbytes)
         _lib.call("dspark_qmm_affine", _ptr(x2), x2.stride(0), m, k, _ptr(w), _ptr(scales),
-                  _ptr(biases), n, bits, group_size, _ptr(out), out.stride(0), _stream(x))
+                  _ptr(biases), n, bits, group_size, _ptr(out), out.stride(0), _ptr(ws),
+                  0 if ws is None else ws.numel(), _stream(x))
     return out.reshape(*lead, n)
 
 
@@ -119,7 +122,10 @@ def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = 
         keep += [x2, w, s, b, y]
         probs[i] = _lib.QmmProblem(_ptr(x2), x2.stride(0), _ptr(w), _ptr(s), _ptr(b), _ptr(y), y.stride(0), n, k)
         results.append(y.reshape(*x.shape[:-1], n))
-    _lib.call("dspark_qmm_affine_multi", probs, cnt, m, bits, group_size, _stream(x_list[0]))
+    nbytes = _lib.load().dspark_qmm_affine_multi_workspace(probs, cnt, m, bits, group_size)
+    ws = qmm_workspace(x_list[0].device, nbytes)
+    _lib.call("dspark_qmm_affine_multi", probs, cnt, m, bits, group_size, _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(x_list[0]))
     return results
 
 
@@ -144,6 +150,26 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _workspaces[key] = buf
+    return buf
+
+
+_qmm_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def qmm_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """The qmm workspace of (device, current stream): zero-filled when allocated (its arrival
+    counters must start at zero; every qmm call leaves them zero). Kept apart from the other
+    scratch buffers, which hold arbitrary data between calls."""
+    if nbytes <= 0:
+        return None
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _qmm_workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        # a replaced buffer is only reused by torch's allocator after this stream's pending work
+        buf = torch.zeros(max(nbytes, 4 << 20), dtype=torch.uint8, device=dev)
+        _qmm_workspaces[key] = buf
     return buf
 
 

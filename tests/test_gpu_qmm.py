@@ -134,3 +134,28 @@ def test_refusals_raise(dev):
     assert lib.dspark_qmm_affine_supported(4, 96, 8, 4, 64) == -2
     assert lib.dspark_qmm_affine_supported(4, 128, 8, 4, 32) == -6
     assert lib.dspark_qmm_affine_supported(16, 4096, 4096, 8, 64) == 0
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_split_k_workspace_reuse_is_bitwise_stable(dev, bits):
+    """Shapes that split K across workgroups share one workspace; its arrival counters must be
+    left at zero by every call, so repeated and interleaved calls give identical bits."""
+    import torch
+
+    from dspark_rocm import _lib, ops
+
+    shapes = [(4096, 4096), (1024, 4096), (4096, 12288), (256, 2048)]
+    inputs = []
+    for i, (n, k) in enumerate(shapes):
+        x, w, s, b = _problem(50 + i, 16, k, n, bits)
+        assert _lib.load().dspark_qmm_affine_workspace(16, k, n, bits, 64) > 0 or n * k < 2**20
+        inputs.append(tuple(t(v, dev) for t, v in zip((to_dev_bf16, to_dev_packed, to_dev_bf16, to_dev_bf16),
+                                                         (x, w, s, b))) + ((x, w, s, b),))
+    first = [ops.quantized_matmul(xd, wd, sd, bd, bits=bits) for xd, wd, sd, bd, _ in inputs]
+    for rep in range(3):
+        for i in ([0, 1, 2, 3] if rep % 2 == 0 else [3, 1, 0, 2]):
+            xd, wd, sd, bd, _ = inputs[i]
+            again = ops.quantized_matmul(xd, wd, sd, bd, bits=bits)
+            assert torch.equal(again, first[i]), (rep, i)
+    for (xd, wd, sd, bd, host), y in zip(inputs, first):
+        _check(from_dev_bf16(y), qmm_ref.qmm_f64(*host, bits), "split-K")
