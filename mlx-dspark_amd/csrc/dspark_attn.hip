@@ -251,25 +251,76 @@ __global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
   }
 }
 
-// out[row, d] = sum_j 2^(m_j - M) o_j[row, d] / sum_j 2^(m_j - M) l_j[row]
+// Combine of the key blocks (multirow_attn.py:162-178): M = max_j m_j, out = sum_j 2^(m_j - M)
+// o_j / sum_j 2^(m_j - M) l_j. One workgroup per (batch*kv-head, row): wave w folds blocks
+// j = w, w+4, ... with an online max, issuing CB blocks' loads per memory round trip; the four
+// wave results are merged in LDS in wave order.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
-  const int bh = blockIdx.x;
-  const int b = bh / a.Hk, hk = bh % a.Hk;
-  const int idx = blockIdx.y * 256 + threadIdx.x;
-  const int row = idx / D, d = idx % D;
-  if (row >= a.R) return;
+  constexpr int DPL = D / 64;  // d values per lane
+  constexpr int CB = 8;        // blocks in flight per wave
+  const int bh = blockIdx.x / a.R, row = blockIdx.x - bh * a.R;
+  const int b = bh / a.Hk, hk = bh - b * a.Hk;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const long base = (long)bh * a.NB * a.RP + row;
-  float M = -1e30f;
-  for (int j = 0; j < a.NB; ++j) M = fmaxf(M, a.mpart[base + (long)j * a.RP]);
-  float num = 0.f, den = 0.f;
-  for (int j = 0; j < a.NB; ++j) {
-    const long pj = base + (long)j * a.RP;
-    const float w = exp2f(a.mpart[pj] - M);
-    den += w * a.lpart[pj];
-    num += w * a.opart[pj * D + d];
+  float M = -1e30f, den = 0.f, num[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) num[t] = 0.f;
+  for (int j0 = wave; j0 < a.NB; j0 += 4 * CB) {  // wave-uniform trip count
+    float mj[CB], lj[CB], oj[CB][DPL];
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int j = min(j0 + 4 * i, a.NB - 1);
+      const long pj = base + (long)j * a.RP;
+      mj[i] = a.mpart[pj];
+      lj[i] = a.lpart[pj];
+      if constexpr (DPL == 2) {
+        const float2 o2 = *reinterpret_cast<const float2*>(&a.opart[pj * D + 2 * lane]);
+        oj[i][0] = o2.x;
+        oj[i][1] = o2.y;
+      } else {
+        oj[i][0] = a.opart[pj * D + lane];
+      }
+    }
+    float mn = M;
+#pragma unroll
+    for (int i = 0; i < CB; ++i)
+      if (j0 + 4 * i < a.NB) mn = fmaxf(mn, mj[i]);
+    const float f = exp2f(M - mn);
+    den *= f;
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) num[t] *= f;
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      if (j0 + 4 * i < a.NB) {
+        const float w = exp2f(mj[i] - mn);
+        den += w * lj[i];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) num[t] += w * oj[i][t];
+      }
+    }
+    M = mn;
   }
-  a.out[((long)(b * a.Hq + hk * a.gqa) * a.Mq + row) * D + d] = f2bf(num / den);
+  __shared__ float sm[4], sd[4], so[4][D];
+  if (lane == 0) {
+    sm[wave] = M;
+    sd[wave] = den;
+  }
+#pragma unroll
+  for (int t = 0; t < DPL; ++t) so[wave][DPL * lane + t] = num[t];
+  __syncthreads();
+  const int d = threadIdx.x;
+  if (d < D) {
+    const float Mx = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+    float nn = 0.f, dd = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = exp2f(sm[w] - Mx);
+      nn += f * so[w][d];
+      dd += f * sd[w];
+    }
+    a.out[((long)(b * a.Hq + hk * a.gqa) * a.Mq + row) * D + d] = f2bf(nn / dd);
+  }
 }
 
 struct Plan {
@@ -393,7 +444,7 @@ extern "C" int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int
   }
   st = check_launch("verify_attention(p1)");
   if (st || p.NB == 1) return st;
-  const dim3 grid2((unsigned)(B * Hk), (unsigned)((p.R * D + 255) / 256));
+  const dim3 grid2((unsigned)(B * Hk * p.R));
   if (D == 128) hipLaunchKernelGGL((attn_combine_kernel<128>), grid2, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((attn_combine_kernel<64>), grid2, dim3(256), 0, s, a);
   return check_launch("verify_attention(combine)");

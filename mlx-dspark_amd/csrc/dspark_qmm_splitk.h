@@ -3,9 +3,12 @@
 // Workgroup = NS waves = NS tiles of 16 output features ("strip" of 16*NS rows) x one slice of
 // K (blockIdx.y). The slice of x (16 rows x slice) is staged once in LDS and shared by the NS
 // waves, together with its per-group row sums (the bias term's sum_j x[m, j], reduced across
-// 8 lanes during staging). Each wave issues every weight load of its 16 rows x slice up front
-// (one 16/8-byte load per row-group per lane, straight from the packed row), loads scales and
-// biases 8 groups per 16-byte load, then runs the MFMA loop reading x fragments from LDS.
+// 8 lanes during staging). Load order is what keeps this a single memory round trip: every
+// x-slice load of the thread is issued first, then every weight load of its 16 rows x slice
+// (one 16/8-byte load per row-group per lane, straight from the packed row), then the scales
+// and biases (8 groups per 16-byte load). Vector-memory completion is counted in issue order,
+// so waiting for x does not wait for the weight stream; the MFMA loop then consumes weights
+// as they land, reading x fragments from LDS.
 // Slices of one strip are combined by the last workgroup to finish (a device-scope arrival
 // counter per strip), always in slice order 0..S-1, so the result is deterministic and
 // independent of M and of arrival order.
@@ -86,7 +89,26 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   const int ncol = strip * 16 * NS + 16 * wave + c16;
   const int n = min(ncol, N - 1);
 
-  // ---- 1. every weight fragment of this lane's row in the slice (clamped, unconditional)
+  // ---- 1. the x slice (16 rows; rows >= M are clamped duplicates): issue every load now.
+  // 16-byte chunk c covers row c / (8*gcount), group (c / 8) % gcount, eighth c % 8; the 8
+  // chunks of one (row, group) sit in 8 consecutive lanes. The chunk count 128*gcount is a
+  // multiple of 64, so each wave either handles a whole iteration or skips it.
+  constexpr int XCH = (2 * KSMAX) / NS;  // max chunks per thread (128 * KSMAX / (64 * NS))
+  static_assert(XCH >= 1 && (2 * KSMAX) % NS == 0, "x staging shape");
+  const int cpr = gcount * 8;  // chunks per row
+  const int xtotal = 16 * cpr;
+  u32x4_t xv[XCH];
+  {
+    const u16* xb = P.x + (long)gs * 64;
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = min(tid + i * 64 * NS, xtotal - 1);
+      const int row = c / cpr, col = c - row * cpr;
+      const int src = m_base + min(row, m_rows - 1);
+      xv[i] = ldg128(xb + (long)src * P.ldx + 8 * col);
+    }
+  }
+  // ---- 2. every weight fragment of this lane's row in the slice (clamped, unconditional)
   WFrag<BITS> wf[KSMAX];
   const u32* wr = wrow_ptr<BITS>(P.w, n, K, q);
 #pragma unroll
@@ -97,7 +119,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     else
       wf[gl].v = ldg128(wr + 16 * g);
   }
-  // ---- 2. scales / biases of the row's groups in the slice
+  // ---- 3. scales / biases of the row's groups in the slice
   constexpr int SBV = (KSMAX + 7) / 8;
   u32x4_t svv[SBV], bvv[SBV];
   u32 svs[SBVEC ? 1 : KSMAX], bvs[SBVEC ? 1 : KSMAX];
@@ -119,33 +141,34 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
       bvs[gl] = brow[g];
     }
   }
-  // ---- 3. the x slice (16 rows; rows >= M are clamped duplicates) -> LDS, with group sums.
-  // 16-byte chunk c covers row c / (8*gcount), group (c / 8) % gcount, eighth c % 8; the 8
-  // chunks of one (row, group) sit in 8 consecutive lanes and are summed with xor-shuffles.
-  {
-    const int cpr = gcount * 8;  // chunks per row
-    const int total = 16 * cpr;  // multiple of 64: every wave runs whole iterations
-    const u16* xb = P.x + (long)gs * 64;
-    for (int c = tid; c < total; c += 64 * NS) {
-      const int row = c / cpr, col = c - row * cpr;
-      const int src = m_base + min(row, m_rows - 1);
-      u32x4_t v = ldg128(xb + (long)src * P.ldx + 8 * col);
-      float s8 = sum_bf16x8(v);
-      s8 += shfl_xor(s8, 1);
-      s8 += shfl_xor(s8, 2);
-      s8 += shfl_xor(s8, 4);
-      if (BITS == 4) {
-        // store the 8 values in the (t, t+4) order unpack_u4 produces
-        v = perm_x_u4(v);
-        s8 *= -128.0f;
-      }
-      *reinterpret_cast<u32x4_t*>(&xs[row * XP + 8 * col]) = v;
-      if ((c & 7) == 0) xsum[(col >> 3) * 16 + row] = s8;
+  // every load above is issued before anything consumes one (keeps the scheduler from
+  // interleaving the x processing, and its waits, into the load sequence)
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- 4. x slice -> LDS with the group sums (8-lane xor-shuffle reduction). Branch-free, so
+  // the compiler cannot sink a load into a conditional block behind the weight stream: a chunk
+  // past the slice (whole waves only) lands in the row's unused 16-byte pad.
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c0 = tid + i * 64 * NS;
+    const bool valid = c0 < xtotal;
+    const int c = min(c0, xtotal - 1);
+    const int row = c / cpr, col = c - row * cpr;
+    u32x4_t v = xv[i];
+    float s8 = sum_bf16x8(v);
+    s8 += shfl_xor(s8, 1);
+    s8 += shfl_xor(s8, 2);
+    s8 += shfl_xor(s8, 4);
+    if (BITS == 4) {
+      // store the 8 values in the (t, t+4) order unpack_u4 produces
+      v = perm_x_u4(v);
+      s8 *= -128.0f;
     }
+    *reinterpret_cast<u32x4_t*>(&xs[row * XP + (valid ? 8 * col : KSMAX * 64)]) = v;
+    if (valid && (c & 7) == 0) xsum[(col >> 3) * 16 + row] = s8;
   }
   __syncthreads();
 
-  // ---- 4. MFMA loop over the slice
+  // ---- 5. MFMA loop over the slice
   constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
   f32x4_t acc = zero;
@@ -179,7 +202,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     }
   }
 
-  // ---- 5. epilogue: lane holds y[m_base + 4q + r][ncol]
+  // ---- 6. epilogue: lane holds y[m_base + 4q + r][ncol]
   if (S == 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
