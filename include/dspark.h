@@ -60,9 +60,10 @@ const char* dspark_last_error(void);
  * y       bf16 [M, N], row stride ldy
  * bits    4 or 8; group_size 64; K % 64 == 0, K <= 32768.
  * workspace  device buffer of at least dspark_qmm_affine_workspace(...) bytes, 256-byte
- *            aligned, whose first part (arrival counters) is ZERO before the first call that
- *            uses it; every call leaves it zero again. NULL is allowed when the size is 0.
- *            Calls sharing one workspace must be ordered on one stream.
+ *            aligned. Its first 256 KiB (arrival counters, the same bytes for every shape)
+ *            must be ZERO before the first call that uses it; every call leaves them zero
+ *            again, so one workspace serves calls of any shapes. NULL is allowed when the size
+ *            is 0. Calls sharing one workspace must be ordered on one stream.
  *
  * Replaces skinny_qmm.qmm(x2, weight, scales, biases, bits) (skinny_qmm.py:239-246), i.e. the
  * `dspark_skinny_qmm` Metal kernel (skinny_qmm.py:56-171) and, outside its window, the stock

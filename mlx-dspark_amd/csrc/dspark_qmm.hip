@@ -34,6 +34,11 @@ namespace {
 constexpr int kNS = 4;             // waves (16-row output tiles) per workgroup: 64-row strips
 constexpr int kStripRows = 16 * kNS;
 constexpr int kTargetWorkgroups = 512;  // two per CU on 256 CUs
+// Split-K arrival counters live in a fixed region at the start of the workspace, the same bytes
+// for every shape, so partials of one shape never land on another shape's counters (each
+// launch leaves its counters at zero).
+constexpr size_t kCtrRegionBytes = 256 * 1024;
+constexpr size_t kMaxCounters = kCtrRegionBytes / sizeof(int);
 
 // Launch plan shared by the workspace query and the launch: S depends only on the strips and
 // K, never on M, so a row's result does not depend on how many rows ride with it.
@@ -64,7 +69,11 @@ Plan make_plan(const long* Ns, int count, long K, long M) {
   p.ksmax = per <= 8 ? 8 : per <= 16 ? 16 : 32;
   if (p.S > 1) {
     const size_t ctrs = (size_t)strips * p.mtiles;
-    p.ctr_bytes = ((ctrs * sizeof(int)) + 255) & ~size_t(255);
+    if (ctrs > kMaxCounters) {
+      p.S = 0;  // refused: more output tiles than counters
+      return p;
+    }
+    p.ctr_bytes = kCtrRegionBytes;
     p.part_bytes = ctrs * p.S * 16 * kStripRows * sizeof(float);
   }
   return p;
@@ -89,7 +98,7 @@ int check_common(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
   if (M < 1 || N < 1 || K < 64) return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   if (K % 64) return fail(DSPARK_ERR_SHAPE, "qmm: K=%lld is not a multiple of 64", (long long)K);
   if (K > 32 * 16 * 64) return fail(DSPARK_ERR_SHAPE, "qmm: K=%lld > 32768", (long long)K);
-  if (M > (1 << 20) || N > (1L << 30) / 16)
+  if (M > 65535L * 16 || N > (1L << 30) / 16)  // 16-row tiles index grid.z
     return fail(DSPARK_ERR_SHAPE, "qmm: shape too large (M=%lld N=%lld)", (long long)M, (long long)N);
   return DSPARK_OK;
 }
@@ -126,7 +135,13 @@ int validate(const dspark_qmm_problem* problems, int count, int64_t M, int bits,
 using namespace dspark;
 
 extern "C" int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
-  return check_common(M, K, N, bits, group_size);
+  const int st = check_common(M, K, N, bits, group_size);
+  if (st) return st;
+  long Ns[1] = {(long)N};
+  if (make_plan(Ns, 1, K, M).S == 0)
+    return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld x N=%lld needs more than %zu split-K counters", (long long)M,
+                (long long)N, kMaxCounters);
+  return DSPARK_OK;
 }
 
 extern "C" size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* problems, int count, int64_t M,
@@ -152,6 +167,8 @@ extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int c
   if (st) return st;
   const long K = problems[0].K;
   const Plan p = make_plan(Ns, count, K, M);
+  if (p.S == 0)
+    return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld needs more than %zu split-K counters", (long long)M, kMaxCounters);
   const size_t need = p.ctr_bytes + p.part_bytes;
   if (need && (!workspace || workspace_bytes < need))
     return fail(DSPARK_ERR_WORKSPACE, "qmm: workspace %zu < %zu bytes", workspace_bytes, need);
