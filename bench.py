@@ -126,7 +126,16 @@ class LayerSet:
         self.weight_bytes = sum(n * k * bits // 8 + 4 * n * (k // 64) for n, k in shapes.values())
         self.gu_bytes = sum(qmm_bytes(*shapes[n], bits, m) for n in ("gate", "up")) - 2 * m * H  # x once
 
-    def step(self, i: int, ev=None) -> None:
+    def gate_up(self, i: int) -> None:
+        """The step's dominant launch: gate and up projections as one two-problem qmm launch."""
+        from dspark_rocm import ops
+
+        L = self.layers[i % len(self.layers)]
+        x, y = self.x, self.y
+        ops.quantized_matmul_multi([x["gu"]], [L["gate"][0], L["up"][0]], [L["gate"][1], L["up"][1]],
+                                   [L["gate"][2], L["up"][2]], bits=self.bits, outs=[y["gate"], y["up"]])
+
+    def step(self, i: int) -> None:
         from dspark_rocm import ops
 
         L = self.layers[i % len(self.layers)]
@@ -134,12 +143,7 @@ class LayerSet:
         ops.quantized_matmul_multi([x["qkv"]], [L[n][0] for n in "qkv"], [L[n][1] for n in "qkv"],
                                    [L[n][2] for n in "qkv"], bits=b, outs=[y["q"], y["k"], y["v"]])
         ops.quantized_matmul(x["o"], *L["o"], bits=b, out=y["o"])
-        if ev is not None:
-            ev[0].record()
-        ops.quantized_matmul_multi([x["gu"]], [L["gate"][0], L["up"][0]], [L["gate"][1], L["up"][1]],
-                                   [L["gate"][2], L["up"][2]], bits=b, outs=[y["gate"], y["up"]])
-        if ev is not None:
-            ev[1].record()
+        self.gate_up(i)
         ops.quantized_matmul(x["down"], *L["down"], bits=b, out=y["down"])
 
 
@@ -369,20 +373,16 @@ def main() -> None:
     # eager, for reference (host-issue bound at these sizes)
     t0 = time.perf_counter()
     eager_ms = time_eager(lambda: [ls.step(i) for i in range(a.layers)], 3) / a.layers
-    # dominant kernel: events around the gate/up launch, every step of an eager replay
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
-    torch.cuda.synchronize()
-    for i in range(K):
-        ls.step(i, ev=evs[i])
-    torch.cuda.synchronize()
-    gu_ms = sorted(e[0].elapsed_time(e[1]) for e in evs)
-    gu_avg = sum(gu_ms) / len(gu_ms)
+    # dominant kernel: K gate/up launches back to back (rotating layers) as one graph, HIP events
+    # on the launch stream around the replay; average launch = total / K
+    gu_total, _ = time_graph(lambda: [ls.gate_up(i) for i in range(K)], 1)
+    gu_avg = gu_total / K
     gu_gbs = ls.gu_bytes / (gu_avg * 1e-3) / 1e9
     log(f"gate/up launch: avg {gu_avg * 1e3:.2f} us, {gu_gbs:.1f} GB/s; eager step {eager_ms * 1e3:.1f} us "
         f"({time.perf_counter() - t0:.1f} s)")
 
     traffic = load_traffic()
-    roofline = {"kernel": "qmm_kernel<8-bit> gate+up launch (N=2x12288, K=4096, M=16)", "bound": "hbm",
+    roofline = {"kernel": "qmm_sk_kernel<8,4,16,true> gate+up launch (N=2x12288, K=4096, M=16; grid 384x4)", "bound": "hbm",
                 "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                 "traffic": (traffic or {}).get("qmm_gate_up_bytes"),
