@@ -84,6 +84,12 @@ size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, int bits, in
  * Mirrors skinny_qmm.fits (skinny_qmm.py:174-181) without launching. */
 int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int bits, int group_size);
 
+/* Launch geometry dspark_qmm_affine uses for this shape (host-only query, no GPU work):
+ * out[0] K slices S, out[1] groups per slice the kernel is built for, out[2] 64-row strips,
+ * out[3] workgroups. Mirrors skinny_qmm.plan / geometry (skinny_qmm.py:190-237), whose
+ * (template, grid, threadgroup) the Python layer caches per module. Returns a dspark_status. */
+int dspark_qmm_affine_plan(int64_t M, int64_t K, int64_t N, int bits, int group_size, int32_t out[4]);
+
 /* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size, M and K
  * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,
  * biases and y. Replaces the per-projection QuantizedLinear calls of one decoder layer
@@ -143,6 +149,13 @@ size_t dspark_verify_attention_workspace(int64_t B, int64_t Hq, int64_t Hk, int6
 
 /* Number of split-KV blocks the launch plan uses for this shape (for tests and reports).
  * Mirrors multirow_attn.plan (multirow_attn.py:204-220) in spirit; the geometry is MI355X's. */
+/* Launch geometry of dspark_verify_attention (host-only query): out[0] rows R = gqa * Mq,
+ * out[1] padded rows RP, out[2] row groups NRG, out[3] keys per block CHUNK, out[4] key
+ * blocks NB, out[5] pass-1 workgroups. Mirrors multirow_attn.plan (multirow_attn.py:204-220).
+ * Returns a dspark_status. */
+int dspark_verify_attention_plan(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D, int64_t L_total,
+                                 int32_t out[6]);
+
 int64_t dspark_verify_attention_blocks(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
                                        int64_t L_total);
 

@@ -376,6 +376,21 @@ extern "C" size_t dspark_verify_attention_workspace(int64_t B, int64_t Hq, int64
   return workspace_bytes(make_plan(B, Hq, Hk, Mq, L_total), B, Hk, D);
 }
 
+extern "C" int dspark_verify_attention_plan(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
+                                            int64_t L_total, int32_t* out) {
+  if (!out) return fail(DSPARK_ERR_ARG, "verify_attention_plan: null output");
+  const int st = check_shape(B, Hq, Mq, D, Hk, L_total);
+  if (st) return st;
+  const Plan p = make_plan(B, Hq, Hk, Mq, L_total);
+  out[0] = p.R;
+  out[1] = p.RP;
+  out[2] = p.NRG;
+  out[3] = p.chunk;
+  out[4] = p.NB;
+  out[5] = (int32_t)(B * Hk * p.NB * p.NRG);
+  return DSPARK_OK;
+}
+
 extern "C" int64_t dspark_verify_attention_blocks(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
                                                   int64_t L_total) {
   if (check_shape(B, Hq, Mq, D, Hk, L_total)) return -1;

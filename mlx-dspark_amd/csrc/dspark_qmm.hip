@@ -144,6 +144,19 @@ extern "C" int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int 
   return DSPARK_OK;
 }
 
+extern "C" int dspark_qmm_affine_plan(int64_t M, int64_t K, int64_t N, int bits, int group_size, int32_t* out) {
+  if (!out) return fail(DSPARK_ERR_ARG, "qmm_plan: null output");
+  const int st = dspark_qmm_affine_supported(M, K, N, bits, group_size);
+  if (st) return st;
+  long Ns[1] = {(long)N};
+  const Plan p = make_plan(Ns, 1, K, M);
+  out[0] = p.S;
+  out[1] = p.ksmax;
+  out[2] = p.strips;
+  out[3] = p.S * p.strips * p.mtiles;
+  return DSPARK_OK;
+}
+
 extern "C" size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* problems, int count, int64_t M,
                                                     int bits, int group_size) {
   long Ns[kQmmMaxProblems];

@@ -72,6 +72,7 @@ SIGNATURES: dict[str, tuple] = {
                                   c_int, c_int, c_void_p, c_i64, c_void_p, c_size_t, c_void_p]),
     "dspark_qmm_affine_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_int, c_int]),
     "dspark_qmm_affine_supported": (c_int, [c_i64, c_i64, c_i64, c_int, c_int]),
+    "dspark_qmm_affine_plan": (c_int, [c_i64, c_i64, c_i64, c_int, c_int, ctypes.POINTER(ctypes.c_int32)]),
     "dspark_qmm_affine_multi": (c_int, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int, c_void_p,
                                         c_size_t, c_void_p]),
     "dspark_qmm_affine_multi_workspace": (c_size_t, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int]),
@@ -80,6 +81,8 @@ SIGNATURES: dict[str, tuple] = {
                                         c_size_t, c_void_p]),
     "dspark_verify_attention_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "dspark_verify_attention_blocks": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "dspark_verify_attention_plan": (c_int, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                             ctypes.POINTER(ctypes.c_int32)]),
     "dspark_moe_route_topk": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_int, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p]),
     "dspark_gather_qmm": (c_int, [c_void_p, c_i64, c_i64, c_void_p, c_void_p, c_i64, c_i64, c_void_p,
