@@ -149,6 +149,17 @@ size_t dspark_verify_attention_workspace(int64_t B, int64_t Hq, int64_t Hk, int6
 
 /* Number of split-KV blocks the launch plan uses for this shape (for tests and reports).
  * Mirrors multirow_attn.plan (multirow_attn.py:204-220) in spirit; the geometry is MI355X's. */
+/* dspark_verify_attention with the output written through element strides
+ * out_strides = {batch, query head, position} (head_dim contiguous; each a multiple of 4), so a
+ * verify forward can write [B, Mq, Hq*D] rows directly as the o_proj input
+ * ({Mq*Hq*D, D, Hq*D}). Same kernels and semantics as dspark_verify_attention. */
+int dspark_verify_attention_strided(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
+                                    const void* k, const void* v, const int64_t k_strides[3],
+                                    const int64_t v_strides[3], int64_t Hk, int64_t L_total, float scale,
+                                    int causal, const uint32_t* tree_anc, void* out,
+                                    const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
+                                    dspark_stream stream);
+
 /* Launch geometry of dspark_verify_attention (host-only query): out[0] rows R = gqa * Mq,
  * out[1] padded rows RP, out[2] row groups NRG, out[3] keys per block CHUNK, out[4] key
  * blocks NB, out[5] pass-1 workgroups. Mirrors multirow_attn.plan (multirow_attn.py:204-220).
@@ -215,6 +226,48 @@ int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t 
                           void* workspace, size_t workspace_bytes, dspark_stream stream);
 
 size_t dspark_moe_workspace(int64_t M, int64_t H, int64_t I, int64_t E, int64_t k);
+
+/* ------------------------------------------------------------------ verify-forward layer kernels */
+
+/*
+ * The elementwise/normalisation steps of a dense verify forward around the qmm and attention
+ * launches: mlx-lm's qwen3-style DecoderLayer as the reference runs it (target.py:187-221
+ * _body_mlxlm -> layer(h, mask, cache), third-party), with mlx's bf16 op rounding.
+ */
+
+/* y[m] = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w) with h = x[m] (r NULL) or
+ * h = bf16(x[m] + r[m]) (residual add; h is also written to h_out when non-NULL).
+ * x, r, h_out, y, w bf16; rows 16-byte aligned, strides % 8 == 0, H % 8 == 0. Replaces
+ * nn.RMSNorm (mx.fast.rms_norm) and the residual `h = x + r` of the decoder layer. */
+int dspark_rmsnorm(const void* x, int64_t ldx, const void* r, int64_t ldr, const void* w, int64_t M, int64_t H,
+                   float eps, void* h_out, int64_t ldh, void* y, int64_t ldy, dspark_stream stream);
+
+/* Per verify row m and head: q/k RMSNorm over head_dim (weights q_norm_w / k_norm_w), RoPE
+ * (non-traditional: pairs (i, i + D/2), angle (pos0 + m) * rope_base^(-2i/D), fp32), then
+ *   q_out [Hq, M, D] (contiguous; the attention q input, batch 1),
+ *   k_cache[h * k_cache_strides[0] + (pos0 + m) * k_cache_strides[1] + d] = rotated k,
+ *   v_cache[...same with v strides...] = v.
+ * q [M, ldq >= Hq*D], k/v [M, ld >= Hk*D] are the q/k/v projections; D in {64, 128}.
+ * Replaces Attention.__call__'s q_norm/k_norm, rope(offset=cache.offset) and
+ * cache.update_and_fetch (mlx-lm qwen3; the cache write of batch_engine.py:193-219). */
+int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                           int64_t M, int64_t Hq, int64_t Hk, int64_t D, const void* q_norm_w,
+                           const void* k_norm_w, float eps, float rope_base, int64_t pos0, void* q_out,
+                           void* k_cache, const int64_t k_cache_strides[2], void* v_cache,
+                           const int64_t v_cache_strides[2], dspark_stream stream);
+
+/* h = bf16(bf16(g * bf16(sigmoid(g))) * u) over [M, N] (N % 8 == 0): MLP's silu(gate) * up. */
+int dspark_swiglu(const void* g, int64_t ldg, const void* u, int64_t ldu, int64_t M, int64_t N, void* h,
+                  int64_t ldh, dspark_stream stream);
+
+/* out[m] = argmax over V of logits[m] (bf16; first index of the maximum). Replaces
+ * mx.argmax(v_logits[0], -1) of the verify loop (generate.py:1548). */
+int dspark_argmax_rows(const void* logits, int64_t ld, int64_t M, int64_t V, int32_t* out, dspark_stream stream);
+
+/* n_accepted[0] = sum(cumprod(draft == target_tokens[:m])) (generate.py:1549-1550): the
+ * accepted draft prefix length; device-side so the round needs one host read. */
+int dspark_greedy_accept(const int32_t* draft, int64_t m, const int32_t* target_tokens, int32_t* n_accepted,
+                         dspark_stream stream);
 
 #ifdef __cplusplus
 }

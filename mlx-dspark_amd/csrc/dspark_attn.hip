@@ -40,6 +40,7 @@ struct AttnArgs {
   u16* out;
   long ksb, ksh, kss;
   long vsb, vsh, vss;
+  long osb, osh, osi;  // output strides (batch, query head, position); head_dim contiguous
   int Hq, Hk, Mq, L;
   int gqa, R, RT, RP;
   int chunk, NB;
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
   if (row >= a.R) return;
   if (a.NB == 1) {
     const float inv = 1.0f / l;
-    u16* orow = a.out + ((long)(b * a.Hq + hk * a.gqa) * a.Mq + row) * D;
+    u16* orow = a.out + b * a.osb + (long)(hk * a.gqa + row / a.Mq) * a.osh + (long)(row % a.Mq) * a.osi;
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
       u32x2_t pk2 = {pack_bf16x2(o[t][0] * inv, o[t][1] * inv), pack_bf16x2(o[t][2] * inv, o[t][3] * inv)};
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
       nn += f * so[w][d];
       dd += f * sd[w];
     }
-    a.out[((long)(b * a.Hq + hk * a.gqa) * a.Mq + row) * D + d] = f2bf(nn / dd);
+    a.out[b * a.osb + (long)(hk * a.gqa + row / a.Mq) * a.osh + (long)(row % a.Mq) * a.osi + d] = f2bf(nn / dd);
   }
 }
 
@@ -397,12 +398,16 @@ extern "C" int64_t dspark_verify_attention_blocks(int64_t B, int64_t Hq, int64_t
   return make_plan(B, Hq, Hk, Mq, L_total).NB;
 }
 
-extern "C" int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D, const void* k,
-                                       const void* v, const int64_t k_strides[3], const int64_t v_strides[3],
-                                       int64_t Hk, int64_t L_total, float scale, int causal,
-                                       const uint32_t* tree_anc, void* out, void* workspace, size_t workspace_bytes_,
-                                       dspark_stream stream) {
-  if (!q || !k || !v || !k_strides || !v_strides || !out) return fail(DSPARK_ERR_ARG, "verify_attention: null pointer");
+namespace {
+int verify_attention_impl(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D, const void* k, const void* v,
+                          const int64_t k_strides[3], const int64_t v_strides[3], int64_t Hk, int64_t L_total,
+                          float scale, int causal, const uint32_t* tree_anc, void* out, const int64_t out_strides[3],
+                          void* workspace, size_t workspace_bytes_, dspark_stream stream) {
+  if (!q || !k || !v || !k_strides || !v_strides || !out || !out_strides)
+    return fail(DSPARK_ERR_ARG, "verify_attention: null pointer");
+  for (int i = 0; i < 3; ++i)
+    if ((out_strides[i] % 4) || out_strides[i] < 0)
+      return fail(DSPARK_ERR_ALIGN, "verify_attention: output strides must be non-negative multiples of 4 elements");
   int st = check_shape(B, Hq, Mq, D, Hk, L_total);
   if (st) return st;
   if (tree_anc && Mq > 32) return fail(DSPARK_ERR_SHAPE, "verify_attention: tree mask needs Mq <= 32");
@@ -429,6 +434,9 @@ extern "C" int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int
   a.vsb = v_strides[0];
   a.vsh = v_strides[1];
   a.vss = v_strides[2];
+  a.osb = out_strides[0];
+  a.osh = out_strides[1];
+  a.osi = out_strides[2];
   a.Hq = (int)Hq;
   a.Hk = (int)Hk;
   a.Mq = (int)Mq;
@@ -463,4 +471,25 @@ extern "C" int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int
   if (D == 128) hipLaunchKernelGGL((attn_combine_kernel<128>), grid2, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((attn_combine_kernel<64>), grid2, dim3(256), 0, s, a);
   return check_launch("verify_attention(combine)");
+}
+}  // namespace
+
+extern "C" int dspark_verify_attention(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D, const void* k,
+                                       const void* v, const int64_t k_strides[3], const int64_t v_strides[3],
+                                       int64_t Hk, int64_t L_total, float scale, int causal,
+                                       const uint32_t* tree_anc, void* out, void* workspace, size_t workspace_bytes_,
+                                       dspark_stream stream) {
+  const int64_t os[3] = {Hq * Mq * D, Mq * D, D};
+  return verify_attention_impl(q, B, Hq, Mq, D, k, v, k_strides, v_strides, Hk, L_total, scale, causal, tree_anc,
+                               out, os, workspace, workspace_bytes_, stream);
+}
+
+extern "C" int dspark_verify_attention_strided(const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
+                                               const void* k, const void* v, const int64_t k_strides[3],
+                                               const int64_t v_strides[3], int64_t Hk, int64_t L_total, float scale,
+                                               int causal, const uint32_t* tree_anc, void* out,
+                                               const int64_t out_strides[3], void* workspace, size_t workspace_bytes_,
+                                               dspark_stream stream) {
+  return verify_attention_impl(q, B, Hq, Mq, D, k, v, k_strides, v_strides, Hk, L_total, scale, causal, tree_anc,
+                               out, out_strides, workspace, workspace_bytes_, stream);
 }

@@ -1,0 +1,314 @@
+// The small kernels a dense verify forward needs around the qmm and attention launches
+// (gfx950): residual add + RMSNorm, per-head q/k RMSNorm + RoPE + KV-cache write, SwiGLU,
+// row argmax and the greedy accept count.
+//
+// Semantics are mlx-lm's qwen3-style decoder layer as the reference runs it
+// (target.py:187-221 -> mlx-lm DecoderLayer, third-party) with mlx's bf16 op rounding:
+//   h  = bf16(x + r)                                     residual add
+//   y  = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w)      RMSNorm (fp32 statistics)
+//   RoPE (non-traditional, pairs (i, i + D/2)), angle a = pos * base^(-2i/D) in fp32:
+//        y_i = bf16(x_i cos a - x_{i+D/2} sin a),  y_{i+D/2} = bf16(x_i sin a + x_{i+D/2} cos a)
+//   h  = bf16(bf16(g * bf16(sigmoid(g))) * u)            SwiGLU (mlx's silu = x * sigmoid(x))
+// and the greedy accept of the verify loop (generate.py:1544-1555):
+//   tt = argmax(logits, -1) (first maximum); n = sum(cumprod(draft == tt[:len(draft)])).
+#include "dspark_common.h"
+
+namespace dspark {
+namespace {
+
+__device__ __forceinline__ float bf16r(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += shfl_xor(v, o);
+  return v;
+}
+
+constexpr int kNormThreads = 256;
+
+// one workgroup per row; 8 bf16 per 16-byte chunk
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const u16* x, long ldx, const u16* __restrict__ r,
+                                                                   long ldr, const u16* __restrict__ w, int H,
+                                                                   float eps, u16* hout, long ldh,
+                                                                   u16* __restrict__ y, long ldy) {
+  __shared__ float red[kNormThreads / 64];
+  const int m = blockIdx.x;
+  const u16* xr = x + (long)m * ldx;
+  const u16* rr = r ? r + (long)m * ldr : nullptr;
+  u16* hr = hout ? hout + (long)m * ldh : nullptr;
+  const int chunks = H >> 3;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < chunks; c += kNormThreads) {
+    u32x4_t xv = ldg128(xr + 8 * c);
+    if (rr) {
+      const u32x4_t rv = ldg128(rr + 8 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xv[i] = pack_bf16x2(bf2f(xv[i] & 0xFFFFu) + bf2f(rv[i] & 0xFFFFu), bf2f(xv[i] >> 16) + bf2f(rv[i] >> 16));
+      if (hr) *reinterpret_cast<u32x4_t*>(hr + 8 * c) = xv;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = bf2f(xv[i] & 0xFFFFu), b = bf2f(xv[i] >> 16);
+      ss += a * a + b * b;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
+  const float inv = 1.0f / __builtin_sqrtf(tot / (float)H + eps);
+  u16* yr = y + (long)m * ldy;
+  for (int c = threadIdx.x; c < chunks; c += kNormThreads) {
+    // the sum h: re-read from h_out when it was written (h_out may alias x: the residual is
+    // then updated in place, and each thread re-reads only chunks it wrote itself)
+    u32x4_t xv = ldg128((hr ? hr : xr) + 8 * c);
+    if (rr && !hr) {
+      const u32x4_t rv = ldg128(rr + 8 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xv[i] = pack_bf16x2(bf2f(xv[i] & 0xFFFFu) + bf2f(rv[i] & 0xFFFFu), bf2f(xv[i] >> 16) + bf2f(rv[i] >> 16));
+    }
+    const u32x4_t wv = ldg128(w + 8 * c);
+    u32x4_t out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = bf16r(bf2f(xv[i] & 0xFFFFu) * inv) * bf2f(wv[i] & 0xFFFFu);
+      const float b = bf16r(bf2f(xv[i] >> 16) * inv) * bf2f(wv[i] >> 16);
+      out[i] = pack_bf16x2(a, b);
+    }
+    *reinterpret_cast<u32x4_t*>(yr + 8 * c) = out;
+  }
+}
+
+struct QkArgs {
+  const u16* q;
+  const u16* k;
+  const u16* v;
+  const u16* qw;
+  const u16* kw;
+  u16* qout;
+  u16* kc;
+  u16* vc;
+  long ldq, ldk, ldv;
+  long kch, kcs, vch, vcs;  // cache strides (head, position) in elements
+  int M, Hq, Hk, pos0;
+  float eps, log2_base;
+};
+
+// one wave per (row, head); lane i < D/2 owns the RoPE pair (i, i + D/2)
+template <int D>
+__global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(const QkArgs a) {
+  constexpr int HALF = D / 2;
+  const int m = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
+  const bool on = lane < HALF;
+  const int i = on ? lane : 0;
+  if (hh >= a.Hq + a.Hk) {  // V head: copy into the cache
+    const int h = hh - a.Hq - a.Hk;
+    const u16* src = a.v + (long)m * a.ldv + (long)h * D;
+    u16* dst = a.vc + (long)h * a.vch + (long)(a.pos0 + m) * a.vcs;
+    if (on) {
+      dst[i] = src[i];
+      dst[i + HALF] = src[i + HALF];
+    }
+    return;
+  }
+  const bool isq = hh < a.Hq;
+  const int h = isq ? hh : hh - a.Hq;
+  const u16* src = isq ? a.q + (long)m * a.ldq + (long)h * D : a.k + (long)m * a.ldk + (long)h * D;
+  const u16* w = isq ? a.qw : a.kw;
+  const float x1 = on ? bf2f(src[i]) : 0.f, x2 = on ? bf2f(src[i + HALF]) : 0.f;
+  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + a.eps);
+  const float n1 = bf16r(bf16r(x1 * inv) * bf2f(w[i]));
+  const float n2 = bf16r(bf16r(x2 * inv) * bf2f(w[i + HALF]));
+  const float inv_freq = exp2f(-(2.0f * (float)i / (float)D) * a.log2_base);
+  const float ang = (float)(a.pos0 + m) * inv_freq;
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  const u16 o1 = f2bf(n1 * cs - n2 * sn), o2 = f2bf(n1 * sn + n2 * cs);
+  if (!on) return;
+  if (isq) {
+    u16* dst = a.qout + ((long)h * a.M + m) * D;
+    dst[i] = o1;
+    dst[i + HALF] = o2;
+  } else {
+    u16* dst = a.kc + (long)h * a.kch + (long)(a.pos0 + m) * a.kcs;
+    dst[i] = o1;
+    dst[i + HALF] = o2;
+  }
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const u16* __restrict__ g, long ldg, const u16* __restrict__ u,
+                                                     long ldu, u16* __restrict__ h, long ldh, int N) {
+  const int m = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;  // 8-element chunk
+  if (8 * c >= N) return;
+  const u32x4_t gv = ldg128(g + (long)m * ldg + 8 * c);
+  const u32x4_t uv = ldg128(u + (long)m * ldu + 8 * c);
+  u32x4_t out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float r[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float gg = bf2f(j ? (gv[i] >> 16) : (gv[i] & 0xFFFFu));
+      const float uu = bf2f(j ? (uv[i] >> 16) : (uv[i] & 0xFFFFu));
+      const float sg = bf16r(1.0f / (1.0f + expf(-gg)));
+      r[j] = bf16r(gg * sg) * uu;
+    }
+    out[i] = pack_bf16x2(r[0], r[1]);
+  }
+  *reinterpret_cast<u32x4_t*>(h + (long)m * ldh + 8 * c) = out;
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+// best by (value desc, index asc); NaN never wins
+__device__ __forceinline__ void arg_better(float& v, int& id, float v2, int id2) {
+  if (v2 > v || (v2 == v && id2 < id)) {
+    v = v2;
+    id = id2;
+  }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const u16* __restrict__ x, long ld, int V,
+                                                                     int32_t* __restrict__ out) {
+  __shared__ float sv[kArgmaxThreads / 64];
+  __shared__ int si[kArgmaxThreads / 64];
+  const int m = blockIdx.x;
+  const u16* row = x + (long)m * ld;
+  float best = -INFINITY;
+  int bid = 0x7FFFFFFF;
+  const int chunks = V >> 3;
+  for (int c = threadIdx.x; c < chunks; c += kArgmaxThreads) {
+    const u32x4_t v = ldg128(row + 8 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      arg_better(best, bid, bf2f(v[i] & 0xFFFFu), 8 * c + 2 * i);
+      arg_better(best, bid, bf2f(v[i] >> 16), 8 * c + 2 * i + 1);
+    }
+  }
+  for (int j = 8 * chunks + threadIdx.x; j < V; j += kArgmaxThreads) arg_better(best, bid, bf2f(row[j]), j);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float v2 = shfl_xor(best, o);
+    const int i2 = __builtin_amdgcn_ds_bpermute((__lane_id() ^ o) << 2, bid);
+    arg_better(best, bid, v2, i2);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = best;
+    si[threadIdx.x >> 6] = bid;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int id = si[0];
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) arg_better(b, id, sv[w], si[w]);
+    out[m] = (id == 0x7FFFFFFF) ? 0 : id;  // an all-NaN row reports token 0
+  }
+}
+
+__global__ void greedy_accept_kernel(const int32_t* __restrict__ draft, int m, const int32_t* __restrict__ tt,
+                                     int32_t* __restrict__ n_out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int n = 0;
+  while (n < m && draft[n] == tt[n]) ++n;
+  n_out[0] = n;
+}
+
+}  // namespace
+}  // namespace dspark
+
+using namespace dspark;
+
+extern "C" int dspark_rmsnorm(const void* x, int64_t ldx, const void* r, int64_t ldr, const void* w, int64_t M,
+                              int64_t H, float eps, void* h_out, int64_t ldh, void* y, int64_t ldy,
+                              dspark_stream stream) {
+  if (!x || !w || !y) return fail(DSPARK_ERR_ARG, "rmsnorm: null pointer");
+  if (M < 1 || H < 8 || H % 8 || M > 65535 || H > (1 << 20)) return fail(DSPARK_ERR_SHAPE, "rmsnorm: M=%lld H=%lld (H %% 8 == 0)", (long long)M, (long long)H);
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || ldx % 8 || ldy % 8 || ldx < H || ldy < H ||
+      (r && (!aligned(r, 16) || ldr % 8 || ldr < H)) || (h_out && (!aligned(h_out, 16) || ldh % 8 || ldh < H)))
+    return fail(DSPARK_ERR_ALIGN, "rmsnorm: rows must be 16-byte aligned with strides %% 8 == 0 and >= H");
+  if (h_out && !r) return fail(DSPARK_ERR_ARG, "rmsnorm: h_out needs a residual r");
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)M), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u16*>(x), (long)ldx, static_cast<const u16*>(r), (long)ldr,
+                     static_cast<const u16*>(w), (int)H, eps, static_cast<u16*>(h_out), (long)ldh,
+                     static_cast<u16*>(y), (long)ldy);
+  return check_launch("rmsnorm");
+}
+
+extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                                      int64_t ldv, int64_t M, int64_t Hq, int64_t Hk, int64_t D, const void* q_norm_w,
+                                      const void* k_norm_w, float eps, float rope_base, int64_t pos0, void* q_out,
+                                      void* k_cache, const int64_t k_cache_strides[2], void* v_cache,
+                                      const int64_t v_cache_strides[2], dspark_stream stream) {
+  if (!q || !k || !v || !q_norm_w || !k_norm_w || !q_out || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides)
+    return fail(DSPARK_ERR_ARG, "qk_norm_rope_kv: null pointer");
+  if (D != 64 && D != 128) return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: head_dim %lld (64 or 128)", (long long)D);
+  if (M < 1 || M > 65535 || Hq < 1 || Hk < 1 || Hq + 2 * Hk > 65535 || pos0 < 0 || pos0 + M > (1L << 30))
+    return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: M=%lld Hq=%lld Hk=%lld pos0=%lld", (long long)M, (long long)Hq,
+                (long long)Hk, (long long)pos0);
+  if (ldq < Hq * D || ldk < Hk * D || ldv < Hk * D || !(rope_base > 0.f))
+    return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: row strides below the head widths or rope_base <= 0");
+  QkArgs a{};
+  a.q = static_cast<const u16*>(q);
+  a.k = static_cast<const u16*>(k);
+  a.v = static_cast<const u16*>(v);
+  a.qw = static_cast<const u16*>(q_norm_w);
+  a.kw = static_cast<const u16*>(k_norm_w);
+  a.qout = static_cast<u16*>(q_out);
+  a.kc = static_cast<u16*>(k_cache);
+  a.vc = static_cast<u16*>(v_cache);
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.ldv = ldv;
+  a.kch = k_cache_strides[0];
+  a.kcs = k_cache_strides[1];
+  a.vch = v_cache_strides[0];
+  a.vcs = v_cache_strides[1];
+  a.M = (int)M;
+  a.Hq = (int)Hq;
+  a.Hk = (int)Hk;
+  a.pos0 = (int)pos0;
+  a.eps = eps;
+  a.log2_base = log2f(rope_base);
+  const dim3 grid((unsigned)M, (unsigned)(Hq + 2 * Hk));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128) hipLaunchKernelGGL(qk_norm_rope_kv_kernel<128>, grid, dim3(64), 0, s, a);
+  else hipLaunchKernelGGL(qk_norm_rope_kv_kernel<64>, grid, dim3(64), 0, s, a);
+  return check_launch("qk_norm_rope_kv");
+}
+
+extern "C" int dspark_swiglu(const void* g, int64_t ldg, const void* u, int64_t ldu, int64_t M, int64_t N, void* h,
+                             int64_t ldh, dspark_stream stream) {
+  if (!g || !u || !h) return fail(DSPARK_ERR_ARG, "swiglu: null pointer");
+  if (M < 1 || M > 65535 || N < 8 || N % 8) return fail(DSPARK_ERR_SHAPE, "swiglu: M=%lld N=%lld (N %% 8 == 0)", (long long)M, (long long)N);
+  if (!aligned(g, 16) || !aligned(u, 16) || !aligned(h, 16) || ldg % 8 || ldu % 8 || ldh % 8 || ldg < N || ldu < N || ldh < N)
+    return fail(DSPARK_ERR_ALIGN, "swiglu: rows must be 16-byte aligned with strides %% 8 == 0 and >= N");
+  const dim3 grid((unsigned)((N / 8 + 255) / 256), (unsigned)M);
+  hipLaunchKernelGGL(swiglu_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const u16*>(g),
+                     (long)ldg, static_cast<const u16*>(u), (long)ldu, static_cast<u16*>(h), (long)ldh, (int)N);
+  return check_launch("swiglu");
+}
+
+extern "C" int dspark_argmax_rows(const void* logits, int64_t ld, int64_t M, int64_t V, int32_t* out,
+                                  dspark_stream stream) {
+  if (!logits || !out) return fail(DSPARK_ERR_ARG, "argmax_rows: null pointer");
+  if (M < 1 || M > 65535 || V < 1 || V >= (1L << 30) || ld < V) return fail(DSPARK_ERR_SHAPE, "argmax_rows: M=%lld V=%lld", (long long)M, (long long)V);
+  if (!aligned(logits, 16) || ld % 8) return fail(DSPARK_ERR_ALIGN, "argmax_rows: rows must be 16-byte aligned (ld %% 8 == 0)");
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)M), dim3(kArgmaxThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u16*>(logits), (long)ld, (int)V, out);
+  return check_launch("argmax_rows");
+}
+
+extern "C" int dspark_greedy_accept(const int32_t* draft, int64_t m, const int32_t* target_tokens, int32_t* n_accepted,
+                                    dspark_stream stream) {
+  if (!target_tokens || !n_accepted || (m > 0 && !draft)) return fail(DSPARK_ERR_ARG, "greedy_accept: null pointer");
+  if (m < 0 || m > (1 << 20)) return fail(DSPARK_ERR_SHAPE, "greedy_accept: m=%lld", (long long)m);
+  hipLaunchKernelGGL(greedy_accept_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), draft, (int)m,
+                     target_tokens, n_accepted);
+  return check_launch("greedy_accept");
+}

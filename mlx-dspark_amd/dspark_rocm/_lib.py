@@ -79,6 +79,9 @@ SIGNATURES: dict[str, tuple] = {
     "dspark_verify_attention": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_i64_p,
                                         c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                         c_size_t, c_void_p]),
+    "dspark_verify_attention_strided": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_i64_p,
+                                                c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p, c_i64_p,
+                                                c_void_p, c_size_t, c_void_p]),
     "dspark_verify_attention_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "dspark_verify_attention_blocks": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "dspark_verify_attention_plan": (c_int, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
@@ -92,6 +95,14 @@ SIGNATURES: dict[str, tuple] = {
                                       c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_size_t, c_void_p]),
     "dspark_moe_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "dspark_rmsnorm": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_float, c_void_p, c_i64,
+                               c_void_p, c_i64, c_void_p]),
+    "dspark_qk_norm_rope_kv": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                       c_void_p, c_void_p, c_float, c_float, c_i64, c_void_p, c_void_p, c_i64_p,
+                                       c_void_p, c_i64_p, c_void_p]),
+    "dspark_swiglu": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p]),
+    "dspark_argmax_rows": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p]),
+    "dspark_greedy_accept": (c_int, [c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,308 @@
+"""Dense qwen3-style target and its verify forward on the gfx950 kernels.
+
+The reference verifies a draft by running its target's forward over ``[anchor] + draft``
+rows against the KV cache (``Target.verify``, target.py:642-677 -> ``run`` / ``_body_mlxlm`` /
+``_head_mlxlm``, :187-221, :347-354): mlx-lm's DecoderLayer stack (third-party) with every
+projection a ``QuantizedLinear`` and every attention call ``mx.fast.scaled_dot_product_attention``.
+
+Two forwards of the same weights live here:
+
+* :meth:`DenseModel.forward` — the module path, op for op the mlx-lm layer on torch tensors:
+  its projections are :class:`~dspark_rocm.nn.QuantizedLinear` calls and its attention goes
+  through :func:`dspark_rocm.fast.scaled_dot_product_attention`, so the reference's scopes
+  (``small_m_matmul``, ``multirow_attention``, ``sdpa_split``) route it exactly as they route
+  mlx-lm. Norms and RoPE are torch ops with the same bf16 rounding points as the kernels.
+* :class:`VerifyEngine` — the MI355X verify step: per layer one fused residual-add + RMSNorm,
+  one q/k/v qmm launch, one q/k-norm + RoPE + cache-write kernel, split-KV attention writing
+  o_proj's input rows directly, the o qmm, residual-add + RMSNorm, one gate/up qmm launch,
+  SwiGLU, the down qmm; then the final norm, lm_head, device argmax and greedy accept. All
+  buffers are preallocated, so a step can be captured in a hipGraph.
+
+:class:`Target` mirrors the reference's ``verify`` / ``rollback`` / ``make_cache`` surface and
+the greedy round (generate.py:1544-1593).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from . import fast, ops
+from .kv_cache import KVCache
+from .nn import QuantizedLinear
+
+
+@dataclass(frozen=True)
+class ModelArgs:
+    hidden_size: int
+    num_hidden_layers: int
+    intermediate_size: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    vocab_size: int
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    bits: int = 8
+    lm_head_bits: int = 8
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """``bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)`` (fp32 statistics)."""
+    xf = x.float()
+    inv = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return ((xf * inv).to(torch.bfloat16).float() * w.float()).to(torch.bfloat16)
+
+
+def rope(x: torch.Tensor, pos0: int, base: float) -> torch.Tensor:
+    """Non-traditional RoPE over the last dim of x [..., L, D] at positions pos0..pos0+L-1."""
+    D = x.shape[-1]
+    half = D // 2
+    i = torch.arange(half, device=x.device, dtype=torch.float32)
+    inv_freq = torch.exp2(-(2.0 * i / D) * math.log2(base))
+    pos = torch.arange(pos0, pos0 + x.shape[-2], device=x.device, dtype=torch.float32)
+    ang = pos[:, None] * inv_freq[None, :]
+    c, s = torch.cos(ang), torch.sin(ang)
+    x1, x2 = x[..., :half].float(), x[..., half:].float()
+    return torch.cat([(x1 * c - x2 * s).to(torch.bfloat16), (x1 * s + x2 * c).to(torch.bfloat16)], dim=-1)
+
+
+class Attention(nn.Module):
+    def __init__(self, args: ModelArgs, q, k, v, o, q_norm, k_norm):
+        super().__init__()
+        self.args = args
+        self.q_proj, self.k_proj, self.v_proj, self.o_proj = q, k, v, o
+        self.register_buffer("q_norm", q_norm)
+        self.register_buffer("k_norm", k_norm)
+
+    def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        a = self.args
+        B, L, _ = x.shape
+        hq, hk, d = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+        q = rms_norm(self.q_proj(x).reshape(B, L, hq, d), self.q_norm, a.rms_norm_eps).transpose(1, 2)
+        k = rms_norm(self.k_proj(x).reshape(B, L, hk, d), self.k_norm, a.rms_norm_eps).transpose(1, 2)
+        v = self.v_proj(x).reshape(B, L, hk, d).transpose(1, 2)
+        q = rope(q, cache.offset, a.rope_theta)
+        k = rope(k, cache.offset, a.rope_theta)
+        keys, values = cache.update_and_fetch(k, v)
+        out = fast.scaled_dot_product_attention(q.contiguous(), keys, values, scale=d ** -0.5,
+                                                mask="causal" if L > 1 else None)
+        return self.o_proj(out.transpose(1, 2).reshape(B, L, hq * d))
+
+
+class MLP(nn.Module):
+    def __init__(self, gate, up, down):
+        super().__init__()
+        self.gate_proj, self.up_proj, self.down_proj = gate, up, down
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        g = self.gate_proj(x)
+        return self.down_proj((g * torch.sigmoid(g)) * self.up_proj(x))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, args: ModelArgs, attn: Attention, mlp: MLP, input_norm, post_norm):
+        super().__init__()
+        self.args = args
+        self.self_attn, self.mlp = attn, mlp
+        self.register_buffer("input_layernorm", input_norm)
+        self.register_buffer("post_attention_layernorm", post_norm)
+
+    def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        eps = self.args.rms_norm_eps
+        h = x + self.self_attn(rms_norm(x, self.input_layernorm, eps), cache)
+        return h + self.mlp(rms_norm(h, self.post_attention_layernorm, eps))
+
+
+class DenseModel(nn.Module):
+    def __init__(self, args: ModelArgs, embed: torch.Tensor, layers: list[DecoderLayer], norm: torch.Tensor,
+                 lm_head: QuantizedLinear):
+        super().__init__()
+        self.args = args
+        self.register_buffer("embed_tokens", embed)
+        self.layers = nn.ModuleList(layers)
+        self.register_buffer("norm", norm)
+        self.lm_head = lm_head
+
+    @classmethod
+    def random(cls, args: ModelArgs, *, device, seed: int = 0) -> "DenseModel":
+        """Random-init weights of this architecture (packed affine weights drawn directly in the
+        packed domain; norm weights near 1; bf16 embedding table)."""
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        H, I, hq, hk, d = (args.hidden_size, args.intermediate_size, args.num_attention_heads,
+                           args.num_key_value_heads, args.head_dim)
+
+        def lin(n, k, bits=args.bits):
+            return QuantizedLinear.random(n, k, bits=bits, device=device, generator=g)
+
+        def normw(n):
+            return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+
+        layers = []
+        for _ in range(args.num_hidden_layers):
+            attn = Attention(args, lin(hq * d, H), lin(hk * d, H), lin(hk * d, H), lin(H, hq * d), normw(d), normw(d))
+            layers.append(DecoderLayer(args, attn, MLP(lin(I, H), lin(I, H), lin(H, I)), normw(H), normw(H)))
+        embed = torch.randn((args.vocab_size, H), generator=g, device=device).to(torch.bfloat16)
+        return cls(args, embed, layers, normw(H), lin(args.vocab_size, H, args.lm_head_bits))
+
+    def make_cache(self, capacity: int = 0) -> list[KVCache]:
+        a = self.args
+        dev = self.embed_tokens.device
+        return [KVCache(1, a.num_key_value_heads, a.head_dim, device=dev, capacity=capacity)
+                for _ in range(a.num_hidden_layers)]
+
+    def forward(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
+        """ids [1, L] -> logits [1, L, V] (the module path)."""
+        h = self.embed_tokens[ids]
+        for layer, c in zip(self.layers, cache):
+            h = layer(h, c)
+        return self.lm_head(rms_norm(h, self.norm, self.args.rms_norm_eps))
+
+
+class VerifyEngine:
+    """Preallocated fused verify step for up to ``max_rows`` rows (batch 1)."""
+
+    def __init__(self, model: DenseModel, max_rows: int = 16):
+        a = model.args
+        self.model, self.args, self.max_rows = model, a, max_rows
+        dev = model.embed_tokens.device
+        H, I, hq, hk, d = (a.hidden_size, a.intermediate_size, a.num_attention_heads, a.num_key_value_heads,
+                           a.head_dim)
+        bf = torch.bfloat16
+        e = lambda *s: torch.empty(s, dtype=bf, device=dev)
+        self.h, self.r, self.y = e(max_rows, H), e(max_rows, H), e(max_rows, H)
+        self.q, self.k, self.v = e(max_rows, hq * d), e(max_rows, hk * d), e(max_rows, hk * d)
+        self.qatt = e(1, hq, max_rows, d)
+        self.att = e(max_rows, hq * d)
+        self.g, self.u, self.hm = e(max_rows, I), e(max_rows, I), e(max_rows, I)
+        self.logits = e(max_rows, a.vocab_size)
+        self.ids = torch.zeros(max_rows, dtype=torch.int64, device=dev)
+        self.tt = torch.zeros(max_rows, dtype=torch.int32, device=dev)
+        self.draft = torch.zeros(max(max_rows - 1, 1), dtype=torch.int32, device=dev)
+        self.n_acc = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(self, M: int, cache: list[KVCache], pos0: int, *, accept: bool = False) -> torch.Tensor:
+        """Run the forward over ``self.ids[:M]`` at cache positions pos0..pos0+M-1 (caches
+        already reserved); logits in ``self.logits[:M]``; with ``accept``, also the target
+        tokens ``self.tt[:M]`` and the accepted count ``self.n_acc`` for ``self.draft[:M-1]``.
+        Enqueues kernels only (graph-capturable for a fixed pos0)."""
+        a, m = self.args, self.model
+        hq, hk, d, eps = a.num_attention_heads, a.num_key_value_heads, a.head_dim, a.rms_norm_eps
+        h, r, y = self.h[:M], self.r[:M], self.y[:M]
+        torch.index_select(m.embed_tokens, 0, self.ids[:M], out=h)
+        L = pos0 + M
+        qatt = self.qatt[:, :, :M]
+        if M != self.max_rows:
+            qatt = self.qatt.view(-1)[:hq * M * d].view(1, hq, M, d)
+        for li, (layer, c) in enumerate(zip(m.layers, cache)):
+            at, mlp = layer.self_attn, layer.mlp
+            if li == 0:
+                ops.rmsnorm(h, layer.input_layernorm, eps, out=y)
+            else:
+                ops.rmsnorm(h, layer.input_layernorm, eps, residual=r, h_out=h, out=y)
+            ops.quantized_matmul_multi([y], [at.q_proj.weight, at.k_proj.weight, at.v_proj.weight],
+                                       [at.q_proj.scales, at.k_proj.scales, at.v_proj.scales],
+                                       [at.q_proj.biases, at.k_proj.biases, at.v_proj.biases], bits=at.q_proj.bits,
+                                       outs=[self.q[:M], self.k[:M], self.v[:M]])
+            ops.qk_norm_rope_kv(self.q[:M], self.k[:M], self.v[:M], at.q_norm, at.k_norm, heads=hq, kv_heads=hk,
+                                head_dim=d, eps=eps, rope_base=a.rope_theta, pos0=pos0, q_out=qatt[0],
+                                k_cache=c.keys[0], v_cache=c.values[0])
+            kv, vv = c.keys[:, :, :L], c.values[:, :, :L]
+            att = self.att[:M]
+            ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1)
+            ops.quantized_matmul(att, at.o_proj.weight, at.o_proj.scales, at.o_proj.biases, bits=at.o_proj.bits, out=r)
+            ops.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
+            ops.quantized_matmul_multi([y], [mlp.gate_proj.weight, mlp.up_proj.weight],
+                                       [mlp.gate_proj.scales, mlp.up_proj.scales],
+                                       [mlp.gate_proj.biases, mlp.up_proj.biases], bits=mlp.gate_proj.bits,
+                                       outs=[self.g[:M], self.u[:M]])
+            ops.swiglu(self.g[:M], self.u[:M], out=self.hm[:M])
+            ops.quantized_matmul(self.hm[:M], mlp.down_proj.weight, mlp.down_proj.scales, mlp.down_proj.biases,
+                                 bits=mlp.down_proj.bits, out=r)
+        ops.rmsnorm(h, m.norm, eps, residual=r, h_out=h, out=y)
+        lm = m.lm_head
+        logits = self.logits[:M]
+        ops.quantized_matmul(y, lm.weight, lm.scales, lm.biases, bits=lm.bits, out=logits)
+        if accept:
+            ops.argmax_rows(logits, out=self.tt[:M])
+            ops.greedy_accept(self.draft[:M - 1], self.tt[:M], out=self.n_acc)
+        return logits
+
+
+class Target:
+    """The reference's Target surface for a dense model: ``make_cache``, ``verify``,
+    ``plain``, ``rollback`` (target.py:166-184, :642-696), plus the greedy round."""
+
+    def __init__(self, model: DenseModel, max_rows: int = 16):
+        self.model = model
+        self.engine = VerifyEngine(model, max_rows)
+        self.max_rows = max_rows
+
+    def make_cache(self, capacity: int = 0) -> list[KVCache]:
+        return self.model.make_cache(capacity)
+
+    def verify(self, ids: torch.Tensor, cache: list[KVCache], tap=None):
+        """ids [1, 1+m] = [anchor] + m drafts -> (logits [1, 1+m, V], None). Writes the rows
+        into every layer's cache (offset advances by 1+m)."""
+        flat = ids.reshape(-1)
+        M = int(flat.numel())
+        if not 1 <= M <= self.max_rows:
+            raise ValueError(f"verify width {M} outside 1..{self.max_rows}")
+        for c in cache:
+            c.reserve(M)
+        pos0 = cache[0].offset
+        self.engine.ids[:M].copy_(flat.to(self.engine.ids.device, torch.int64))
+        logits = self.engine.step(M, cache, pos0)
+        for c in cache:
+            c.advance(M)
+        return logits.reshape(1, M, -1), None
+
+    def plain(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
+        return self.verify(ids, cache)[0]
+
+    def rollback(self, cache: list[KVCache], n_rejected: int, accepted=None) -> None:
+        """Dense rollback: trim every cache by the rejected rows; 0 is a no-op."""
+        if n_rejected > 0:
+            for c in cache:
+                if c is not None and hasattr(c, "trim"):
+                    c.trim(n_rejected)
+
+    def greedy_round(self, pending: int, draft: list[int], cache: list[KVCache]) -> tuple[int, list[int]]:
+        """One speculative round (generate.py:1544-1593): verify [pending] + draft, argmax and
+        accept on the device, one host read, rollback of the rejected rows. Returns
+        (n accepted drafts, committed tokens = accepted drafts + the target's bonus token)."""
+        e = self.engine
+        M = 1 + len(draft)
+        if M > self.max_rows:
+            raise ValueError(f"verify width {M} > {self.max_rows}")
+        for c in cache:
+            c.reserve(M)
+        pos0 = cache[0].offset
+        e.ids[:M].copy_(torch.tensor([pending] + list(draft), dtype=torch.int64))
+        if draft:
+            e.draft[:M - 1].copy_(torch.tensor(draft, dtype=torch.int32))
+        e.step(M, cache, pos0, accept=True)
+        for c in cache:
+            c.advance(M)
+        tt = e.tt[:M].tolist()                    # the round's one host read
+        n = int(e.n_acc.item()) if draft else 0
+        self.rollback(cache, len(draft) - n)
+        return n, list(draft[:n]) + [int(tt[n])]
+
+
+def greedy_generate(target: Target, prompt: list[int], steps: int) -> list[int]:
+    """Plain greedy decoding (one token per forward): the reference output speculative
+    decoding must reproduce."""
+    cache = target.make_cache(len(prompt) + steps + 16)
+    logits = None
+    for i in range(0, len(prompt), target.max_rows):
+        logits, _ = target.verify(torch.tensor([prompt[i:i + target.max_rows]]), cache)
+    out = [int(torch.argmax(logits[0, -1].float()))]
+    while len(out) < steps:
+        logits, _ = target.verify(torch.tensor([[out[-1]]]), cache)
+        out.append(int(torch.argmax(logits[0, -1].float())))
+    return out

@@ -294,3 +294,88 @@ def moe_switch_glu(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: 
               _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu), _ptr(su), _ptr(bu), _ptr(wd), _ptr(sd), _ptr(bd),
               bits, group_size, _ptr(out), _ptr(inds), _ptr(scores), _ptr(ws), ws.numel(), _stream(x))
     return out, inds, scores
+
+
+def verify_attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, out_strides, *,
+                          scale: float, causal: bool = True, tree_anc: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`verify_attention` writing through element strides ``out_strides`` = (batch, query
+    head, position) of ``out`` (head_dim contiguous), e.g. [B, Mq, Hq*D] rows for o_proj."""
+    _require_cuda(q, k, v, out)
+    B, Hq, mq, D = q.shape
+    Hk, L = k.shape[1], k.shape[2]
+    q = q.contiguous()
+    nbytes = _lib.load().dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
+    ws = workspace(q.device, nbytes)
+    anc = None if tree_anc is None else tree_anc.to(device=q.device, dtype=torch.int32).contiguous()
+    os_ = (ctypes.c_int64 * 3)(*[int(s) for s in out_strides])
+    _lib.call("dspark_verify_attention_strided", _ptr(q), B, Hq, mq, D, _ptr(k), _ptr(v), _i64x3(k), _i64x3(v), Hk, L,
+              float(scale), int(bool(causal)), _ptr(anc), _ptr(out), os_, _ptr(ws), 0 if ws is None else ws.numel(),
+              _stream(q))
+    return out
+
+
+# ---------------------------------------------------------------------------- verify-forward layer ops
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, *, residual: torch.Tensor | None = None,
+            h_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w)`` per row, h = x or bf16(x + residual)
+    (written to ``h_out`` when given). x [M, H] bf16."""
+    _require_cuda(x, w)
+    _require_bf16("x", x)
+    M, H = x.shape
+    if out is None:
+        out = torch.empty((M, H), dtype=torch.bfloat16, device=x.device)
+    _lib.call("dspark_rmsnorm", _ptr(x), x.stride(0), _ptr(residual), 0 if residual is None else residual.stride(0),
+              _ptr(w), M, H, float(eps), _ptr(h_out), 0 if h_out is None else h_out.stride(0), _ptr(out),
+              out.stride(0), _stream(x))
+    return out
+
+
+def qk_norm_rope_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
+                    k_norm_w: torch.Tensor, *, heads: int, kv_heads: int, head_dim: int, eps: float,
+                    rope_base: float, pos0: int, q_out: torch.Tensor, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor) -> torch.Tensor:
+    """q/k RMSNorm + RoPE at positions pos0.. and the cache write. q [M, Hq*D], k/v [M, Hk*D];
+    q_out [Hq, M, D]; k_cache/v_cache [Hk, capacity, D] views (batch 1)."""
+    _require_cuda(q, k, v, q_out, k_cache, v_cache)
+    M = q.shape[0]
+    if k_cache.shape[1] < pos0 + M or v_cache.shape[1] < pos0 + M:
+        raise ValueError(f"cache capacity {k_cache.shape[1]} < pos0 + M = {pos0 + M}")
+    ks = (ctypes.c_int64 * 2)(k_cache.stride(0), k_cache.stride(1))
+    vs = (ctypes.c_int64 * 2)(v_cache.stride(0), v_cache.stride(1))
+    _lib.call("dspark_qk_norm_rope_kv", _ptr(q), q.stride(0), _ptr(k), k.stride(0), _ptr(v), v.stride(0), M, heads,
+              kv_heads, head_dim, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), float(rope_base), int(pos0),
+              _ptr(q_out), _ptr(k_cache), ks, _ptr(v_cache), vs, _stream(q))
+    return q_out
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``bf16(bf16(g * bf16(sigmoid(g))) * u)`` (mlx's silu(g) * u)."""
+    _require_cuda(g, u)
+    M, N = g.shape
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=g.device)
+    _lib.call("dspark_swiglu", _ptr(g), g.stride(0), _ptr(u), u.stride(0), M, N, _ptr(out), out.stride(0), _stream(g))
+    return out
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 [M]: first index of each row's maximum (bf16 logits [M, V])."""
+    _require_cuda(logits)
+    _require_bf16("logits", logits)
+    M, V = logits.shape
+    if out is None:
+        out = torch.empty(M, dtype=torch.int32, device=logits.device)
+    _lib.call("dspark_argmax_rows", _ptr(logits), logits.stride(0), M, V, _ptr(out), _stream(logits))
+    return out
+
+
+def greedy_accept(draft: torch.Tensor, target_tokens: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 [1]: length of the accepted draft prefix (draft == target_tokens[:m] while equal)."""
+    _require_cuda(target_tokens)
+    m = int(draft.numel())
+    if out is None:
+        out = torch.empty(1, dtype=torch.int32, device=target_tokens.device)
+    d = draft.to(device=target_tokens.device, dtype=torch.int32).contiguous() if m else None
+    _lib.call("dspark_greedy_accept", _ptr(d), m, _ptr(target_tokens), _ptr(out), _stream(target_tokens))
+    return out

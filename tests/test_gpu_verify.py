@@ -1,0 +1,184 @@
+"""GPU: the dense verify forward (C5's path) against the oracle.
+
+- layer kernels (residual + RMSNorm, q/k norm + RoPE + cache write, SwiGLU, argmax, greedy
+  accept) against oracle/model_ref.py, moe_ref.swiglu and verify_ref (bit-exact for indices);
+- Target.verify (fused engine) logits against the numpy forward of the same weights over
+  several verify blocks with rollback (max|d| <= 5e-2 * RMS for the whole two-layer forward,
+  greedy tokens equal wherever the top-2 margin exceeds the error); the module path under the
+  reference's scopes against the fused engine;
+- the fixed-seed synthetic speculative trace: tokens committed by greedy speculative rounds
+  equal plain greedy decoding, and the mean accepted length equals the one the draft's
+  corruption pattern implies (generate.py:1544-1593, :111-113).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _model_util import tiny_model, to_ref
+from _util import assert_rms_close
+from oracle import model_ref, moe_ref, verify_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def test_rmsnorm_kernel(dev):
+    from dspark_rocm import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn((16, 5120), generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn((16, 5120), generator=g, device=dev).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(5120, generator=g, device=dev)).to(torch.bfloat16)
+    y = ops.rmsnorm(x, w, 1e-6)
+    assert np.array_equal(_np(y), model_ref.rmsnorm(_np(x), _np(w), 1e-6)) or \
+        np.abs(_np(y) - model_ref.rmsnorm(_np(x), _np(w), 1e-6)).max() <= 2 ** -7 * np.abs(_np(y)).max()
+    h_ref = model_ref.bf(_np(x) + _np(r))
+    hh = x.clone()
+    y2 = ops.rmsnorm(hh, w, 1e-6, residual=r, h_out=hh)              # in place, as the engine runs it
+    assert np.array_equal(_np(hh), h_ref)
+    assert np.abs(_np(y2) - model_ref.rmsnorm(h_ref, _np(w), 1e-6)).max() <= 2 ** -7 * np.abs(h_ref).max()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_qk_norm_rope_kv_kernel(dev, D):
+    from dspark_rocm import ops
+
+    M, Hq, Hk, pos0, cap = 16, 8, 2, 16384, 16384 + 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(D)
+    q = torch.randn((M, Hq * D), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((M, Hk * D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((M, Hk * D), generator=g, device=dev).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kc = torch.zeros((Hk, cap, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    qo = torch.empty((Hq, M, D), dtype=torch.bfloat16, device=dev)
+    ops.qk_norm_rope_kv(q, k, v, qw, kw, heads=Hq, kv_heads=Hk, head_dim=D, eps=1e-6, rope_base=1e6, pos0=pos0,
+                        q_out=qo, k_cache=kc, v_cache=vc)
+    pos = np.arange(pos0, pos0 + M)
+    qr = model_ref.rope(model_ref.rmsnorm(_np(q).reshape(M, Hq, D).transpose(1, 0, 2), _np(qw), 1e-6), pos, 1e6)
+    kr = model_ref.rope(model_ref.rmsnorm(_np(k).reshape(M, Hk, D).transpose(1, 0, 2), _np(kw), 1e-6), pos, 1e6)
+    tol = 2 ** -6 * max(np.abs(qr).max(), 1.0)                      # bf16 ulps of the fp32 angle path
+    assert np.abs(_np(qo) - qr).max() <= tol
+    assert np.abs(_np(kc[:, pos0:pos0 + M]) - kr).max() <= tol
+    assert np.array_equal(_np(vc[:, pos0:pos0 + M]), _np(v).reshape(M, Hk, D).transpose(1, 0, 2))
+    assert not kc[:, :pos0].any() and not kc[:, pos0 + M:].any()   # nothing outside the block
+
+
+def test_swiglu_argmax_accept_kernels(dev):
+    from dspark_rocm import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    a = (3 * torch.randn((16, 4096), generator=g, device=dev)).to(torch.bfloat16)
+    b = torch.randn((16, 4096), generator=g, device=dev).to(torch.bfloat16)
+    assert np.array_equal(_np(ops.swiglu(a, b)), moe_ref.swiglu(_np(a), _np(b)))
+    logits = torch.randn((6, 151936), generator=g, device=dev).to(torch.bfloat16)
+    logits[2, 77] = 50.0
+    logits[2, 9000] = 50.0                                          # tie: the first index wins
+    logits[4, 151935] = 60.0                                        # the last element
+    tt = ops.argmax_rows(logits)
+    want = [int(np.argmax(r)) for r in _np(logits)]
+    assert tt.cpu().tolist() == want and want[2] == 77 and want[4] == 151935
+    for draft, tts in (([5, 6, 7], [5, 6, 9, 1]), ([1, 2], [1, 2, 3]), ([4], [5, 6]), ([], [8])):
+        n = ops.greedy_accept(torch.tensor(draft, dtype=torch.int32), torch.tensor(tts, dtype=torch.int32, device=dev))
+        assert int(n.item()) == verify_ref.greedy_accept(draft, tts)[0]
+
+
+def test_fused_verify_matches_oracle_with_rollback(dev):
+    from dspark_rocm.model import Target
+
+    model = tiny_model(dev, seed=5)
+    ref = to_ref(model)
+    tgt = Target(model)
+    cache = tgt.make_cache(128)
+    r = np.random.Generator(np.random.PCG64(0))
+    blocks = [r.integers(0, 512, n).tolist() for n in (16, 9, 16, 1, 12)]
+    rejects = [0, 5, 15, 0, 3]
+    for ids, rej in zip(blocks, rejects):
+        got, _ = tgt.verify(torch.tensor([ids]), cache)
+        want = ref.forward(ids)
+        # whole forward: each op is within its kernel's bar; ~10 bf16 rounding points per layer
+        # compound, so the logits get 5e-2 * RMS and the greedy tokens must agree wherever the
+        # top-2 margin exceeds that error
+        err, _ = assert_rms_close(_np(got[0]), want, 5e-2, f"verify block of {len(ids)}")
+        top2 = np.sort(want, axis=-1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2 * err
+        assert np.array_equal(_np(got[0]).argmax(-1)[clear], want.argmax(-1)[clear])
+        tgt.rollback(cache, rej)
+        ref.trim(rej)
+        assert cache[0].offset == ref.offset
+
+
+def test_rollback_then_verify_is_bitwise_a_fresh_prefix(dev):
+    from dspark_rocm.model import Target
+
+    model = tiny_model(dev, seed=6)
+    tgt = Target(model)
+    a = tgt.make_cache(64)
+    tgt.verify(torch.tensor([list(range(10, 26))]), a)              # 16 rows
+    tgt.rollback(a, 11)                                              # keep 5
+    la, _ = tgt.verify(torch.tensor([[1, 2, 3, 4]]), a)
+    b = tgt.make_cache(64)
+    tgt.verify(torch.tensor([list(range(10, 15))]), b)
+    lb, _ = tgt.verify(torch.tensor([[1, 2, 3, 4]]), b)
+    assert torch.equal(la, lb)
+
+
+def test_module_path_under_scopes_matches_fused(dev):
+    from dspark_rocm import multirow_attn as mra
+    from dspark_rocm import small_m_qmm as sm
+    from dspark_rocm.model import Target
+
+    model = tiny_model(dev, seed=7)
+    tgt = Target(model)
+    ids = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5, 8, 9, 7, 9, 3]])      # 16 rows: attention eligible
+    ca, cb = tgt.make_cache(64), tgt.make_cache(64)
+    fused, _ = tgt.verify(ids, ca)
+    a = model.args
+    cfg = mra.MultirowConfig((mra.Window(a.num_attention_heads, a.num_key_value_heads, a.head_dim, min_q=2,
+                                         max_q=16, min_kv=16),))
+    ids_all = sm.ids_for_shapes([sm.shape_key(m) for m in model.modules() if sm.eligible(m)], model)
+    with sm.small_m_matmul(ids_all), mra.multirow_attention(cfg), torch.no_grad():
+        mod = model(ids.to(dev), cb)
+    assert_rms_close(_np(mod[0]), _np(fused[0]), 5e-2, "module path vs fused")
+
+
+def test_speculative_trace_is_lossless_with_expected_accept_length(dev):
+    """Drafts are the plain-greedy continuation with seeded corruptions; every round must
+    commit exactly the greedy tokens and accept up to the first corrupted draft token."""
+    from dspark_rocm.model import Target, greedy_generate
+
+    model = tiny_model(dev, seed=8)
+    tgt = Target(model)
+    prompt = [11, 22, 33, 44, 55]
+    steps = 60
+    greedy = greedy_generate(tgt, prompt, steps + 16)
+    r = np.random.Generator(np.random.PCG64(12))
+    cache = tgt.make_cache(len(prompt) + steps + 40)
+    for i in range(0, len(prompt), 16):
+        tgt.verify(torch.tensor([prompt[i:i + 16]]), cache)
+    out = [greedy[0]]
+    rounds, expected_acc = 0, []
+    while len(out) < steps:
+        cap = int(r.integers(1, 8))
+        truth = greedy[len(out):len(out) + cap]
+        draft = [t if r.random() > 0.3 else (t + 1) % 512 for t in truth]
+        n_expect = next((j for j, (d, t) in enumerate(zip(draft, truth)) if d != t), len(draft))
+        n, committed = tgt.greedy_round(out[-1], draft, cache)
+        assert n == n_expect, (rounds, draft, truth)
+        out += committed
+        expected_acc.append(n + 1)
+        rounds += 1
+        assert cache[0].offset == len(prompt) + len(out) - 1
+    assert out[:steps] == greedy[:steps]
+    # the first token came from the prompt's forward; the rounds committed the rest
+    assert verify_ref.mean_accept_len(sum(expected_acc), rounds) == (len(out) - 1) / rounds

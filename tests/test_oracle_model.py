@@ -1,0 +1,66 @@
+"""Pins oracle/model_ref.py: RMSNorm and RoPE closed forms and invariants, rollback semantics of
+the numpy forward, and agreement of the numpy forward with the torch module path of the same
+weights on the CPU (two independent implementations of mlx-lm's decoder semantics)."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from _model_util import tiny_model, to_ref
+from oracle import model_ref, quant_ref
+
+
+def test_rmsnorm_closed_form():
+    x = np.full((2, 64), 3.0, dtype=np.float32)
+    x[1] = -0.5
+    w = np.linspace(0.5, 1.5, 64).astype(np.float32)
+    y = model_ref.rmsnorm(x, quant_ref.bf16_round(w), 1e-6)
+    assert np.allclose(y[0], quant_ref.bf16_round(w), rtol=2 ** -7)
+    assert np.allclose(y[1], -quant_ref.bf16_round(w), rtol=2 ** -7)
+    r = np.random.Generator(np.random.PCG64(0)).standard_normal((3, 128)).astype(np.float32)
+    yy = model_ref.rmsnorm(quant_ref.bf16_round(r), np.ones(128, np.float32), 1e-6)
+    assert np.allclose(np.sqrt((yy.astype(np.float64) ** 2).mean(-1)), 1.0, atol=1e-2)
+
+
+def test_rope_invariants():
+    r = np.random.Generator(np.random.PCG64(1))
+    x = quant_ref.bf16_round(r.standard_normal((2, 5, 128)).astype(np.float32))
+    assert np.array_equal(model_ref.rope(x[:, :1], [0], 1e6), x[:, :1])            # position 0: identity
+    y = model_ref.rope(x, np.arange(5) + 1000, 1e6)
+    n0 = x[..., :64] ** 2 + x[..., 64:] ** 2
+    n1 = y[..., :64].astype(np.float64) ** 2 + y[..., 64:].astype(np.float64) ** 2
+    assert np.allclose(n1, n0, rtol=2e-2, atol=1e-3)                              # rotations keep pair norms
+    q, k = x[0, :1], x[1, :1]
+    dots = [float(np.sum(model_ref.rope(q, [p + 7], 1e4).astype(np.float64) *
+                         model_ref.rope(k, [p], 1e4).astype(np.float64))) for p in (0, 33, 500)]
+    assert max(dots) - min(dots) < 0.05 * np.abs(q).sum()                         # relative position only
+
+
+def test_numpy_forward_matches_torch_module_path_on_cpu():
+    model = tiny_model("cpu", seed=3)
+    ref = to_ref(model)
+    cache = model.make_cache(64)
+    ids = [5, 17, 200, 3, 99, 41]
+    with torch.no_grad():
+        got = model(torch.tensor([ids]), cache)[0].float().numpy()
+    want = ref.forward(ids)
+    rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+    assert np.abs(got - want).max() <= 2e-2 * rms
+    # a second verify block at offset 6 over the cached rows
+    with torch.no_grad():
+        got2 = model(torch.tensor([[7, 8, 9]]), cache)[0].float().numpy()
+    want2 = ref.forward([7, 8, 9])
+    assert np.abs(got2 - want2).max() <= 2e-2 * np.sqrt(np.mean(want2.astype(np.float64) ** 2))
+
+
+def test_rollback_equals_fresh_prefix():
+    model = tiny_model("cpu", seed=4)
+    a = to_ref(model)
+    a.forward([1, 2, 3, 4, 5])
+    a.trim(2)                                    # keep [1, 2, 3]
+    la = a.forward([9, 10])
+    b = to_ref(model)
+    b.forward([1, 2, 3])
+    lb = b.forward([9, 10])
+    assert np.array_equal(la, lb)
