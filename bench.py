@@ -65,9 +65,9 @@ def time_graph(fn, reps: int, warm: int = 3):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        fn()  # allocate anything lazily allocated outside the capture
+        fn()  # per-stream workspaces are allocated (and zeroed) here, outside the capture
     torch.cuda.synchronize()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         fn()
     torch.cuda.synchronize()
     g.replay()
@@ -258,6 +258,52 @@ def bench_moe(dev, m=16, E=128, k=8, H=2048, I=768, bits=4, reps: int = 30):
             "GBs_chained": round(by / us / 1e3, 1)}
 
 
+def bench_verify_forward(dev, context: int = 16384, rows: int = 16, reps: int = 10):
+    """C5: one speculative verify step of a random-init dense 8-bit 64-layer target (hidden
+    5120, heads 64/8 x 128, intermediate 25600, vocab 151936, RoPE 1e6) with `rows` verify rows
+    over a `context`-row synthetic bf16 KV cache: the forward, lm_head, device argmax and
+    greedy accept, captured as one hipGraph (the KV write lands at the same positions each
+    replay); rollback is cache metadata on the host."""
+    import torch
+
+    from dspark_rocm import roofline
+    from dspark_rocm.model import DenseModel, ModelArgs, Target
+
+    args = ModelArgs(hidden_size=5120, num_hidden_layers=64, intermediate_size=25600, num_attention_heads=64,
+                     num_key_value_heads=8, head_dim=128, vocab_size=151936, rope_theta=1e6, bits=8, lm_head_bits=8)
+    t0 = time.perf_counter()
+    model = DenseModel.random(args, device=dev, seed=5)
+    tgt = Target(model, max_rows=rows)
+    cache = tgt.make_cache(context + rows)
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    for c in cache:                       # synthetic KV at depth (calibrate.py:214-244 does the same)
+        c.keys[:, :, :context].normal_(generator=g)
+        c.values[:, :, :context].normal_(generator=g)
+        c.offset = context
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    e = tgt.engine
+    e.ids[:rows].copy_(torch.randint(0, args.vocab_size, (rows,), generator=g, device=dev))
+    e.draft[:rows - 1].copy_(e.ids[1:rows].to(torch.int32))
+
+    def step():
+        e.step(rows, cache, context, accept=True)
+
+    ms, _ = time_graph(step, reps)
+    H, I, hq, hk, d = 5120, 25600, 64, 8, 128
+    per_layer = sum(roofline.qmm_param_bytes(n, k, 8) for n, k in
+                    ((hq * d, H), (hk * d, H), (hk * d, H), (H, hq * d), (I, H), (I, H), (H, I)))
+    weights = 64 * per_layer + roofline.qmm_param_bytes(args.vocab_size, H, 8)
+    kv = 64 * roofline.attention_bytes(hq, hk, d, rows, context + rows)
+    by = weights + kv
+    n = int(e.n_acc.item())
+    return {"layers": 64, "hidden": H, "context": context, "rows": rows, "weight_bytes": weights, "kv_bytes": kv,
+            "bytes": by, "ms_graph": round(ms, 4), "GBs": round(by / (ms * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "accepted": n,
+            "launches": 64 * 10 + 5, "build_s": round(build_s, 1)}
+
+
 def cpu_baseline(bits: int, m: int) -> dict:
     """The C restatement (oracle/dspark_oracle.c, OpenMP) on one layer set of the same shapes."""
     import numpy as np
@@ -312,6 +358,7 @@ def main() -> None:
     ap.add_argument("--layers", type=int, default=8, help="distinct layers in the rotated pool")
     ap.add_argument("--quick", action="store_true", help="skip the C1/C3/C4 extras and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c5", action="store_true", help="skip the full 64-layer verify-forward extra")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (for scaling rocprof byte counters)")
     a = ap.parse_args()
@@ -406,6 +453,12 @@ def main() -> None:
         r = bench_moe(dev)
         extra["C4"] = r
         log(f"C4 MoE: {r['us_chained']} us ({r['GBs_chained']} GB/s), {r['distinct_experts']} experts")
+        if not a.no_c5:
+            r = bench_verify_forward(dev)
+            extra["C5"] = r
+            log(f"C5 verify step (64 layers, 16 rows @ 16k): {r['ms_graph']} ms ({r['GBs']} GB/s, "
+                f"{r['frac_of_peak']:.1%} of peak), {r['bytes'] / 1e9:.2f} GB/step; built in {r['build_s']} s")
+            torch.cuda.empty_cache()
 
     cpu = None
     if not a.quick and not a.no_cpu:

@@ -49,6 +49,7 @@ CASES = [
     (1, 4, 1, 3, 23, 64),         # MQA, tail shorter than a tile
     (1, 32, 8, 1, 300, 128),      # plain decode row
     (1, 24, 4, 8, 1037, 128),
+    (1, 64, 8, 16, 4112, 128),    # the 64/8-head verify forward's shape: 128 rows, 2 row groups
 ]
 
 
