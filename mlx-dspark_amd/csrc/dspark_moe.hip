@@ -16,7 +16,7 @@
 // (counting sort, stable in pair id). The grouped qmm launches one workgroup per
 // (expert, 16-feature tile); workgroups of unselected experts exit at once, every selected
 // expert's weight tile is streamed once for all of its tokens (<= 16 at verify widths).
-#include "dspark_qmm_core.h"
+#include "dspark_moe_sk.h"
 
 namespace dspark {
 namespace {
@@ -30,26 +30,34 @@ struct RouteArgs {
   int* offsets;
   int* sorted;
   int* pos;
+  int* ctr;   // nullable: arrival counters of the grouped qmm, cleared here
+  int nctr;
   int M, E, k, renorm;
 };
 
 __device__ __forceinline__ float bf16r(float f) { return bf2f(f2bf(f)); }
 
-// max by (value desc, id asc)
-__device__ __forceinline__ void argbest(float& v, int& id, float v2, int id2) {
-  if (v2 > v || (v2 == v && id2 < id)) {
-    v = v2;
-    id = id2;
-  }
+// v2/e2 ranks before v/e: larger logit, or equal logit and smaller id
+__device__ __forceinline__ bool ranks_before(float v2, int e2, float v, int e) {
+  return v2 > v || (v2 == v && e2 < e);
 }
 
+// One 1024-thread workgroup routes all M tokens (a wave per token, 16 at a time) and buckets
+// the (token, slot) pairs by expert. NPL = experts per lane (E <= 64 * NPL).
+template <int NPL>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArgs a) {
   extern __shared__ int lds[];
-  int* pair_e = lds;                 // [M*k]
-  int* counts = lds + a.M * a.k;     // [kRouteThreads]
+  int* pair_e = lds;                                                 // [M*k]
+  int* counts = lds + a.M * a.k;                                     // [kRouteThreads]
+  float* gsel = reinterpret_cast<float*>(counts + kRouteThreads);   // [16][32]
+  u32* tmask = reinterpret_cast<u32*>(gsel + 16 * 32);               // [2][kRouteThreads] token bits (M <= 64)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int P = a.M * a.k;
-  constexpr int NPL = 16;  // experts per lane (E <= 1024)
+
+  for (int i = threadIdx.x; i < a.nctr; i += kRouteThreads) a.ctr[i] = 0;
+  counts[threadIdx.x] = 0;
+  tmask[threadIdx.x] = 0;
+  tmask[kRouteThreads + threadIdx.x] = 0;
 
   for (int t = wave; t < a.M; t += kRouteThreads / 64) {
     float xv[NPL];
@@ -69,49 +77,58 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
       if (lane + 64 * i < a.E) sum += expf(xv[i] - mx);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
-    // all lanes now hold the same fp32 sum (same xor tree on every lane)
-    u32 taken = 0;
-    float gsel[32];
-    float gsum = 0.f;
-    for (int j = 0; j < a.k; ++j) {
-      float bv = -INFINITY;
-      int bid = 1 << 30;
+    // rank of each of this lane's experts: how many experts rank before it
+    int rank[NPL];
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        const int e = lane + 64 * i;
-        if (e < a.E && !((taken >> i) & 1u)) argbest(bv, bid, xv[i], e);
-      }
+    for (int i = 0; i < NPL; ++i) rank[i] = 0;
 #pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const float v2 = shfl_xor(bv, o);
-        const int id2 = __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, bid);
-        argbest(bv, bid, v2, id2);
+    for (int i2 = 0; i2 < NPL; ++i2) {
+      const int vb = __builtin_bit_cast(int, xv[i2]);
+      for (int l2 = 0; l2 < 64; ++l2) {
+        const int e2 = l2 + 64 * i2;
+        const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vb, l2));
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) rank[i] += (e2 < a.E && ranks_before(v2, e2, xv[i], lane + 64 * i)) ? 1 : 0;
       }
-      if ((bid & 63) == lane) taken |= 1u << (bid >> 6);
-      const float g = bf16r(expf(bv - mx) / sum);
-      gsel[j] = g;
-      gsum += g;
-      if (lane == 0) a.inds[t * a.k + j] = bid;
-      if (lane == 0) pair_e[t * a.k + j] = bid;
     }
-    const float denom = bf16r(gsum);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < a.E && rank[i] < a.k) {
+        a.inds[t * a.k + rank[i]] = e;
+        pair_e[t * a.k + rank[i]] = e;
+        gsel[wave * 32 + rank[i]] = bf16r(expf(xv[i] - mx) / sum);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
     if (lane == 0) {
+      float gsum = 0.f;
+      for (int j = 0; j < a.k; ++j) gsum += gsel[wave * 32 + j];
+      const float denom = bf16r(gsum);
       for (int j = 0; j < a.k; ++j) {
-        const float s = a.renorm ? bf16r(gsel[j] / denom) : gsel[j];
-        a.scores[t * a.k + j] = f2bf(s);
+        const float g = gsel[wave * 32 + j];
+        a.scores[t * a.k + j] = f2bf(a.renorm ? bf16r(g / denom) : g);
       }
     }
+    __builtin_amdgcn_wave_barrier();
   }
   if (!a.offsets) return;
-  // ---- bucket the (token, slot) pairs by expert, stable in pair id: thread e walks the pairs
-  // in order twice (count, then place); the bucket starts come from an LDS prefix scan.
+  // ---- bucket the (token, slot) pairs by expert, stable in pair id. A token selects an
+  // expert at most once, so a pair's place in its bucket is the number of earlier tokens that
+  // selected the same expert.
+  __syncthreads();
+  const bool bits = a.M <= 64;
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
+    const int pe = pair_e[p], t = p / a.k;
+    if (bits) atomicOr(&tmask[(t >> 5) * kRouteThreads + pe], 1u << (t & 31));
+    else atomicAdd(&counts[pe], 1);
+  }
   __syncthreads();
   const int e = threadIdx.x;
-  int cnt = 0;
-  if (e < a.E)
-    for (int p = 0; p < P; ++p) cnt += (pair_e[p] == e);
-  counts[e] = (e < a.E) ? cnt : 0;  // E <= 1024 == kRouteThreads
+  if (bits) counts[e] = __builtin_popcount(tmask[e]) + __builtin_popcount(tmask[kRouteThreads + e]);
   __syncthreads();
+  const int cnt = counts[e];
   for (int d = 1; d < kRouteThreads; d <<= 1) {  // inclusive Hillis-Steele scan
     const int add = (e >= d) ? counts[e - d] : 0;
     __syncthreads();
@@ -119,16 +136,22 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     __syncthreads();
   }
   if (e < a.E) {
-    const int start = counts[e] - cnt;
-    a.offsets[e] = start;
+    a.offsets[e] = counts[e] - cnt;
     if (e == a.E - 1) a.offsets[a.E] = counts[e];
-    int r = start;
-    for (int p = 0; p < P; ++p)
-      if (pair_e[p] == e) {
-        if (a.sorted) a.sorted[r] = p;
-        if (a.pos) a.pos[p] = r;
-        ++r;
-      }
+  }
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
+    const int pe = pair_e[p], t = p / a.k;
+    int before = 0;
+    if (bits) {
+      const u32 lo = tmask[pe], hi = tmask[kRouteThreads + pe];
+      before = (t < 32) ? __builtin_popcount(lo & ((1u << t) - 1u))
+                        : __builtin_popcount(lo) + __builtin_popcount(hi & ((1u << (t - 32)) - 1u));
+    } else {
+      for (int p2 = 0; p2 < p; ++p2) before += (pair_e[p2] == pe);
+    }
+    const int slot = (pe > 0 ? counts[pe - 1] : 0) + before;  // bucket start + earlier pairs
+    if (a.sorted) a.sorted[slot] = p;
+    if (a.pos) a.pos[p] = slot;
   }
 }
 
@@ -302,8 +325,13 @@ int check_route(long M, long E, long k) {
 }
 
 int launch_route(const RouteArgs& a, hipStream_t s) {
-  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + kRouteThreads);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), lds, s, a);
+  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + 3 * kRouteThreads + 16 * 32);
+  const dim3 g(1), b(kRouteThreads);
+  if (a.E <= 64) hipLaunchKernelGGL(moe_route_kernel<1>, g, b, lds, s, a);
+  else if (a.E <= 128) hipLaunchKernelGGL(moe_route_kernel<2>, g, b, lds, s, a);
+  else if (a.E <= 256) hipLaunchKernelGGL(moe_route_kernel<4>, g, b, lds, s, a);
+  else if (a.E <= 512) hipLaunchKernelGGL(moe_route_kernel<8>, g, b, lds, s, a);
+  else hipLaunchKernelGGL(moe_route_kernel<16>, g, b, lds, s, a);
   return check_launch("moe_route_topk");
 }
 
@@ -335,12 +363,41 @@ int check_qmm_format(long K, long N, int bits, int group_size) {
 
 inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
+// Launch plan of the grouped split-K qmm (moe_sk_kernel) for one projection of every expert.
+struct MoePlan {
+  int S, ksmax, strips, mtiles;
+  bool sbvec;
+  size_t ctrs, part_floats;
+};
+
+MoePlan moe_plan(long K, long N, long E, long M, bool swiglu) {
+  MoePlan p{};
+  const long G = K / 64;
+  p.strips = (int)(swiglu ? (N + 31) / 32 : (N + 63) / 64);
+  p.mtiles = (int)((M + 15) / 16);  // a token selects an expert at most once: <= M rows per bucket
+  long s = (G + 15) / 16;
+  if (E * p.strips * p.mtiles * s < 512) s = (G + 7) / 8;
+  if (s > kQmmMaxSlices) s = kQmmMaxSlices;
+  if (s < (G + 31) / 32) s = (G + 31) / 32;
+  if (s < 1) s = 1;
+  p.S = (int)s;
+  const long per = (G + s - 1) / s;
+  p.ksmax = per <= 8 ? 8 : per <= 16 ? 16 : 32;
+  p.sbvec = (G % s == 0) && ((G / s) % 8 == 0);
+  p.ctrs = (size_t)E * p.strips * p.mtiles;
+  p.part_floats = p.S > 1 ? p.ctrs * p.S * 1024 : 0;
+  return p;
+}
+
 struct MoeWorkspace {
-  size_t offsets, sorted, pos, inds, scores, h, y, total;
+  size_t offsets, sorted, pos, inds, scores, h, y, ctr, part, total;
+  MoePlan gu, dn;
 };
 
 MoeWorkspace moe_layout(long M, long H, long I, long E, long k) {
   MoeWorkspace w{};
+  w.gu = moe_plan(H, I, E, M, true);
+  w.dn = moe_plan(I, H, E, M, false);
   const size_t P = (size_t)M * k;
   size_t o = 0;
   w.offsets = o; o += align256(sizeof(int) * (E + 1));
@@ -350,8 +407,24 @@ MoeWorkspace moe_layout(long M, long H, long I, long E, long k) {
   w.scores = o;  o += align256(sizeof(u16) * P);
   w.h = o;       o += align256(sizeof(u16) * P * I);
   w.y = o;       o += align256(sizeof(u16) * P * H);
+  w.ctr = o;     o += align256(sizeof(int) * (w.gu.ctrs > w.dn.ctrs ? w.gu.ctrs : w.dn.ctrs));
+  w.part = o;    o += align256(sizeof(float) * (w.gu.part_floats > w.dn.part_floats ? w.gu.part_floats : w.dn.part_floats));
   w.total = o;
   return w;
+}
+
+template <bool SWIGLU>
+int launch_moe_sk(const MoeSkArgs& a, const MoePlan& p, int E, int bits, hipStream_t s) {
+  const dim3 grid((unsigned)p.strips, (unsigned)p.S, (unsigned)(E * p.mtiles));
+#define MOE_SK(B, KS, SB) hipLaunchKernelGGL((moe_sk_kernel<B, KS, SB, SWIGLU>), grid, dim3(256), 0, s, a)
+#define MOE_SK_BITS(B)                                                   \
+  if (p.ksmax == 8) { if (p.sbvec) MOE_SK(B, 8, true); else MOE_SK(B, 8, false); }     \
+  else if (p.ksmax == 16) { if (p.sbvec) MOE_SK(B, 16, true); else MOE_SK(B, 16, false); } \
+  else { if (p.sbvec) MOE_SK(B, 32, true); else MOE_SK(B, 32, false); }
+  if (bits == 4) { MOE_SK_BITS(4) } else { MOE_SK_BITS(8) }
+#undef MOE_SK_BITS
+#undef MOE_SK
+  return check_launch(SWIGLU ? "moe gate/up" : "moe down");
 }
 
 }  // namespace
@@ -425,6 +498,10 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   if (st) return st;
   if ((st = check_qmm_format(H, I, bits, group_size))) return st;
   if ((st = check_qmm_format(I, H, bits, group_size))) return st;
+  if (H > 32 * 16 * 64 || I > 32 * 16 * 64)
+    return fail(DSPARK_ERR_SHAPE, "moe_switch_glu: H=%lld I=%lld (each <= 32768)", (long long)H, (long long)I);
+  if (E * ((I + 31) / 32) * ((M + 15) / 16) > 65535L * 64 || (M + 15) / 16 * E > 65535)
+    return fail(DSPARK_ERR_SHAPE, "moe_switch_glu: too many experts x tiles");
   if (!aligned(x, 16) || !aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(out, 2))
     return fail(DSPARK_ERR_ALIGN, "moe_switch_glu: x and packed weights must be 16-byte aligned");
   const MoeWorkspace L = moe_layout(M, H, I, E, k);
@@ -452,10 +529,14 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   r.E = (int)E;
   r.k = (int)k;
   r.renorm = renorm ? 1 : 0;
+  int* ctr = reinterpret_cast<int*>(ws + L.ctr);
+  r.ctr = ctr;  // the grouped qmm's arrival counters start every block at zero
+  r.nctr = (int)(L.gu.ctrs > L.dn.ctrs ? L.gu.ctrs : L.dn.ctrs);
   if ((st = launch_route(r, s))) return st;
 
   const int P = (int)(M * k);
-  GatherArgs g{};
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  MoeSkArgs g{};
   g.x = static_cast<const u16*>(x);
   g.row_index = sorted;
   g.offsets = offsets;
@@ -466,15 +547,20 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   g.s1 = static_cast<const u16*>(s_up);
   g.b1 = static_cast<const u16*>(b_up);
   g.y = h;
+  g.part = part;
+  g.ctr = ctr;
   g.ldx = H;
   g.ldy = I;
   g.K = (int)H;
   g.N = (int)I;
   g.row_div = (int)k;
   g.P_max = P;
-  if ((st = launch_gather<kSwiGLU>(g, (int)E, bits, s))) return st;
+  g.strips = L.gu.strips;
+  g.mtiles = L.gu.mtiles;
+  g.S = L.gu.S;
+  if ((st = launch_moe_sk<true>(g, L.gu, (int)E, bits, s))) return st;
 
-  GatherArgs d{};
+  MoeSkArgs d{};
   d.x = h;
   d.row_index = nullptr;
   d.offsets = offsets;
@@ -482,13 +568,18 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   d.s0 = static_cast<const u16*>(s_down);
   d.b0 = static_cast<const u16*>(b_down);
   d.y = ypair;
+  d.part = part;
+  d.ctr = ctr;
   d.ldx = I;
   d.ldy = H;
   d.K = (int)I;
   d.N = (int)H;
   d.row_div = 1;
   d.P_max = P;
-  if ((st = launch_gather<kPlain>(d, (int)E, bits, s))) return st;
+  d.strips = L.dn.strips;
+  d.mtiles = L.dn.mtiles;
+  d.S = L.dn.S;
+  if ((st = launch_moe_sk<false>(d, L.dn, (int)E, bits, s))) return st;
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)M, (unsigned)((H + 255) / 256)), dim3(256), 0, s, ypair, pos,
                      scores_ws, static_cast<u16*>(out), (int)H, (int)k);
