@@ -37,13 +37,35 @@ struct RouteArgs {
 
 __device__ __forceinline__ float bf16r(float f) { return bf2f(f2bf(f)); }
 
-// v2/e2 ranks before v/e: larger logit, or equal logit and smaller id
-__device__ __forceinline__ bool ranks_before(float v2, int e2, float v, int e) {
-  return v2 > v || (v2 == v && e2 < e);
+// Routing key of expert e with bf16 logit bits b: orders by logit (NaN as -inf, -0 as +0),
+// then by smaller expert id, as one unsigned 32-bit value (larger = chosen first).
+__device__ __forceinline__ u32 route_key(u32 b, int e) {
+  if ((b & 0x7F80u) == 0x7F80u && (b & 0x7Fu)) b = 0xFF80u;
+  if (b == 0x8000u) b = 0u;
+  const u32 ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+  return (ord << 16) | (0xFFFFu - (u32)e);
+}
+// logit (as float) of a routing key
+__device__ __forceinline__ float route_key_logit(u32 key) {
+  const u32 ord = key >> 16;
+  return bf2f((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu));
+}
+
+// Maximum of v over the wave: DPP within each row of 16 lanes, then the four row results.
+__device__ __forceinline__ u32 wave_max_u32(u32 v) {
+  v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+  v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+  v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const u32 r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const u32 r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
 }
 
 // One 1024-thread workgroup routes all M tokens (a wave per token, 16 at a time) and buckets
 // the (token, slot) pairs by expert. NPL = experts per lane (E <= 64 * NPL).
+// Top-k: k rounds of a wave-wide maximum over the routing keys; slot j holds the j-th largest
+// (ties to the smaller id), the order of the reference's descending sort.
 template <int NPL>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArgs a) {
   extern __shared__ int lds[];
@@ -61,43 +83,39 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
 
   for (int t = wave; t < a.M; t += kRouteThreads / 64) {
     float xv[NPL];
-    float mx = -INFINITY;
+    u32 key[NPL];
+    u32 kmax = 0;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const int e = lane + 64 * i;
-      const float lv = (e < a.E) ? bf2f(a.logits[(long)t * a.E + e]) : -INFINITY;
-      xv[i] = (lv == lv) ? lv : -INFINITY;  // NaN ranks last, so a valid expert is always chosen
-      mx = fmaxf(mx, xv[i]);
+      const u32 b = (e < a.E) ? (u32)a.logits[(long)t * a.E + e] : 0xFF80u;
+      key[i] = (e < a.E) ? route_key(b, e) : 0u;  // every real key is > 0
+      xv[i] = route_key_logit(key[i]);
+      kmax = max(kmax, key[i]);
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+    u32 m = wave_max_u32(kmax);
+    const float mx = route_key_logit(m);
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i)
       if (lane + 64 * i < a.E) sum += expf(xv[i] - mx);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
-    // rank of each of this lane's experts: how many experts rank before it
-    int rank[NPL];
+    for (int j = 0; j < a.k; ++j) {
+      if (j > 0) {
+        kmax = 0;
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) rank[i] = 0;
-#pragma unroll
-    for (int i2 = 0; i2 < NPL; ++i2) {
-      const int vb = __builtin_bit_cast(int, xv[i2]);
-      for (int l2 = 0; l2 < 64; ++l2) {
-        const int e2 = l2 + 64 * i2;
-        const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vb, l2));
-#pragma unroll
-        for (int i = 0; i < NPL; ++i) rank[i] += (e2 < a.E && ranks_before(v2, e2, xv[i], lane + 64 * i)) ? 1 : 0;
+        for (int i = 0; i < NPL; ++i) kmax = max(kmax, key[i]);
+        m = wave_max_u32(kmax);
       }
-    }
+      const int e = 0xFFFF - (int)(m & 0xFFFFu);
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < a.E && rank[i] < a.k) {
-        a.inds[t * a.k + rank[i]] = e;
-        pair_e[t * a.k + rank[i]] = e;
-        gsel[wave * 32 + rank[i]] = bf16r(expf(xv[i] - mx) / sum);
+      for (int i = 0; i < NPL; ++i)
+        if (lane + 64 * i == e) key[i] = 0u;
+      if (lane == 0) {
+        a.inds[t * a.k + j] = e;
+        pair_e[t * a.k + j] = e;
+        gsel[wave * 32 + j] = bf16r(expf(route_key_logit(m) - mx) / sum);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -125,20 +143,30 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     else atomicAdd(&counts[pe], 1);
   }
   __syncthreads();
-  const int e = threadIdx.x;
-  if (bits) counts[e] = __builtin_popcount(tmask[e]) + __builtin_popcount(tmask[kRouteThreads + e]);
+  if (bits) counts[threadIdx.x] = __builtin_popcount(tmask[threadIdx.x]) + __builtin_popcount(tmask[kRouteThreads + threadIdx.x]);
   __syncthreads();
-  const int cnt = counts[e];
-  for (int d = 1; d < kRouteThreads; d <<= 1) {  // inclusive Hillis-Steele scan
-    const int add = (e >= d) ? counts[e - d] : 0;
-    __syncthreads();
-    counts[e] += add;
-    __syncthreads();
+  // exclusive scan of the bucket sizes by wave 0, 64 experts at a time; counts[e] becomes the
+  // bucket start
+  if (wave == 0) {
+    int carry = 0;
+    for (int c0 = 0; c0 < a.E; c0 += 64) {
+      const int e = c0 + lane;
+      const int cnt = (e < a.E) ? counts[e] : 0;
+      int incl = cnt;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+      }
+      if (e < a.E) {
+        a.offsets[e] = carry + incl - cnt;
+        counts[e] = carry + incl - cnt;
+      }
+      carry += __shfl(incl, 63);
+    }
+    if (lane == 0) a.offsets[a.E] = carry;
   }
-  if (e < a.E) {
-    a.offsets[e] = counts[e] - cnt;
-    if (e == a.E - 1) a.offsets[a.E] = counts[e];
-  }
+  __syncthreads();
   for (int p = threadIdx.x; p < P; p += kRouteThreads) {
     const int pe = pair_e[p], t = p / a.k;
     int before = 0;
@@ -149,7 +177,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     } else {
       for (int p2 = 0; p2 < p; ++p2) before += (pair_e[p2] == pe);
     }
-    const int slot = (pe > 0 ? counts[pe - 1] : 0) + before;  // bucket start + earlier pairs
+    const int slot = counts[pe] + before;  // bucket start + earlier pairs
     if (a.sorted) a.sorted[slot] = p;
     if (a.pos) a.pos[p] = slot;
   }
@@ -370,7 +398,7 @@ struct MoePlan {
   size_t ctrs, part_floats;
 };
 
-MoePlan moe_plan(long K, long N, long E, long M, bool swiglu) {
+MoePlan moe_plan(long K, long N, long E, long M, bool swiglu, int bits) {
   MoePlan p{};
   const long G = K / 64;
   p.strips = (int)(swiglu ? (N + 31) / 32 : (N + 63) / 64);
@@ -381,8 +409,7 @@ MoePlan moe_plan(long K, long N, long E, long M, bool swiglu) {
   if (s < (G + 31) / 32) s = (G + 31) / 32;
   if (s < 1) s = 1;
   p.S = (int)s;
-  const long per = (G + s - 1) / s;
-  p.ksmax = per <= 8 ? 8 : per <= 16 ? 16 : 32;
+  p.ksmax = slice_capacity(G, s, bits);
   p.sbvec = (G % s == 0) && ((G / s) % 8 == 0);
   p.ctrs = (size_t)E * p.strips * p.mtiles;
   p.part_floats = p.S > 1 ? p.ctrs * p.S * 1024 : 0;
@@ -394,10 +421,11 @@ struct MoeWorkspace {
   MoePlan gu, dn;
 };
 
-MoeWorkspace moe_layout(long M, long H, long I, long E, long k) {
+// (bits only picks the kernel instantiation; the sizes do not depend on it)
+MoeWorkspace moe_layout(long M, long H, long I, long E, long k, int bits) {
   MoeWorkspace w{};
-  w.gu = moe_plan(H, I, E, M, true);
-  w.dn = moe_plan(I, H, E, M, false);
+  w.gu = moe_plan(H, I, E, M, true, bits);
+  w.dn = moe_plan(I, H, E, M, false, bits);
   const size_t P = (size_t)M * k;
   size_t o = 0;
   w.offsets = o; o += align256(sizeof(int) * (E + 1));
@@ -483,7 +511,7 @@ extern "C" int dspark_gather_qmm(const void* x, int64_t ldx, int64_t K, const in
 
 extern "C" size_t dspark_moe_workspace(int64_t M, int64_t H, int64_t I, int64_t E, int64_t k) {
   if (check_route(M, E, k)) return 0;
-  return moe_layout(M, H, I, E, k).total;
+  return moe_layout(M, H, I, E, k, 4).total;
 }
 
 extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t H, int64_t I, int64_t E,
@@ -504,7 +532,7 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
     return fail(DSPARK_ERR_SHAPE, "moe_switch_glu: too many experts x tiles");
   if (!aligned(x, 16) || !aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(out, 2))
     return fail(DSPARK_ERR_ALIGN, "moe_switch_glu: x and packed weights must be 16-byte aligned");
-  const MoeWorkspace L = moe_layout(M, H, I, E, k);
+  const MoeWorkspace L = moe_layout(M, H, I, E, k, bits);
   if (!workspace || workspace_bytes < L.total)
     return fail(DSPARK_ERR_WORKSPACE, "moe_switch_glu: workspace %zu < %zu bytes", workspace_bytes, L.total);
   if (!aligned(workspace, 256)) return fail(DSPARK_ERR_ALIGN, "moe_switch_glu: workspace must be 256-byte aligned");

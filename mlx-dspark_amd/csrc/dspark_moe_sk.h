@@ -50,7 +50,9 @@ __global__ __launch_bounds__(256) void moe_sk_kernel(const MoeSkArgs a) {
   const int m_rows = min(16, p1 - p0);
   const int S = a.S, K = a.K, N = a.N;
   const int G = K >> 6;
-  const int gs = (sl * G) / S, ge = ((sl + 1) * G) / S, gcount = ge - gs;
+  int gs, ge;
+  slice_groups<BITS>(sl, S, G, gs, ge);
+  const int gcount = ge - gs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q = lane >> 4;
   // output column this lane's tile row maps to, and which matrix it reads
@@ -76,16 +78,8 @@ __global__ __launch_bounds__(256) void moe_sk_kernel(const MoeSkArgs a) {
     xv[i] = ldg128(a.x + (long)src * a.ldx + (long)gs * 64 + 8 * col);
   }
   // ---- 2. weights of this lane's row in the slice
-  WFrag<BITS> wf[KSMAX];
-  const u32* wr = wrow_ptr<BITS>(wmat, n, K, q);
-#pragma unroll
-  for (int gl = 0; gl < KSMAX; ++gl) {
-    const int g = gs + min(gl, gcount - 1);
-    if constexpr (BITS == 4)
-      wf[gl].v = ldg64(wr + 8 * g);
-    else
-      wf[gl].v = ldg128(wr + 16 * g);
-  }
+  WSlice<BITS, KSMAX> wsl;
+  wsl.load(wmat + (long)n * (K * BITS / 32), q, gs, gcount, G);
   // ---- 3. scales / biases
   constexpr int SBV = (KSMAX + 7) / 8;
   u32x4_t svv[SBV], bvv[SBV];
@@ -129,23 +123,15 @@ __global__ __launch_bounds__(256) void moe_sk_kernel(const MoeSkArgs a) {
   }
   __syncthreads();
   // ---- 5. MFMA over the slice
-  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4_t acc = zero;
-  const u16* xl = &xs[c16 * XP + 16 * q];
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const u16* xl = &xs[c16 * XP + k_quarter<BITS>(q)];
+  u32x2_t w4[2] = {};
 #pragma unroll
   for (int gl = 0; gl < KSMAX; ++gl) {
     if (gl < gcount) {
+      if (BITS == 4 && (gl & 1) == 0) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
       const u32x4_t a0 = lds128(xl + 64 * gl), a1 = lds128(xl + 64 * gl + 8);
       const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[gl * 16 + 4 * q]);
-      f32x4_t p;
-      if constexpr (BITS == 4) {
-        p = mfma16x16x32(a0, unpack_u4(wf[gl].v.x), c);
-        p = mfma16x16x32(a1, unpack_u4(wf[gl].v.y), p);
-      } else {
-        p = mfma16x16x32(a0, unpack_u8(wf[gl].v.x, wf[gl].v.y), zero);
-        p = mfma16x16x32(a1, unpack_u8(wf[gl].v.z, wf[gl].v.w), p);
-      }
       u32 sbits, bbits;
       if constexpr (SBVEC) {
         sbits = bf_field(svv[gl >> 3], gl & 7);
@@ -154,9 +140,7 @@ __global__ __launch_bounds__(256) void moe_sk_kernel(const MoeSkArgs a) {
         sbits = svs[gl];
         bbits = bvs[gl];
       }
-      const float sf = bf2f(sbits), bf = bf2f(bbits) * bias_mul;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bf, c[r], __builtin_fmaf(sf, p[r], acc[r]));
+      group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : gl], w4[gl & 1], bf2f(sbits), bf2f(bbits), acc);
     }
   }
   // ---- 6. epilogue. tile column t (0..63) of this workgroup = wave * 16 + c16

@@ -51,7 +51,7 @@ struct Plan {
   size_t part_bytes;
 };
 
-Plan make_plan(const long* Ns, int count, long K, long M) {
+Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
   Plan p{};
   const long G = K / 64;
   long strips = 0;
@@ -65,8 +65,7 @@ Plan make_plan(const long* Ns, int count, long K, long M) {
   if (s < (G + 31) / 32) s = (G + 31) / 32;  // a slice holds at most 32 groups
   if (s < 1) s = 1;
   p.S = (int)s;
-  const long per = (G + s - 1) / s;
-  p.ksmax = per <= 8 ? 8 : per <= 16 ? 16 : 32;
+  p.ksmax = slice_capacity(G, s, bits);
   if (p.S > 1) {
     const size_t ctrs = (size_t)strips * p.mtiles;
     if (ctrs > kMaxCounters) {
@@ -138,7 +137,7 @@ extern "C" int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int 
   const int st = check_common(M, K, N, bits, group_size);
   if (st) return st;
   long Ns[1] = {(long)N};
-  if (make_plan(Ns, 1, K, M).S == 0)
+  if (make_plan(Ns, 1, K, M, bits).S == 0)
     return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld x N=%lld needs more than %zu split-K counters", (long long)M,
                 (long long)N, kMaxCounters);
   return DSPARK_OK;
@@ -149,7 +148,7 @@ extern "C" int dspark_qmm_affine_plan(int64_t M, int64_t K, int64_t N, int bits,
   const int st = dspark_qmm_affine_supported(M, K, N, bits, group_size);
   if (st) return st;
   long Ns[1] = {(long)N};
-  const Plan p = make_plan(Ns, 1, K, M);
+  const Plan p = make_plan(Ns, 1, K, M, bits);
   out[0] = p.S;
   out[1] = p.ksmax;
   out[2] = p.strips;
@@ -161,14 +160,14 @@ extern "C" size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* pr
                                                     int bits, int group_size) {
   long Ns[kQmmMaxProblems];
   if (validate(problems, count, M, bits, group_size, Ns)) return 0;
-  const Plan p = make_plan(Ns, count, problems[0].K, M);
+  const Plan p = make_plan(Ns, count, problems[0].K, M, bits);
   return p.ctr_bytes + p.part_bytes;
 }
 
 extern "C" size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
   if (check_common(M, K, N, bits, group_size)) return 0;
   long Ns[1] = {(long)N};
-  const Plan p = make_plan(Ns, 1, K, M);
+  const Plan p = make_plan(Ns, 1, K, M, bits);
   return p.ctr_bytes + p.part_bytes;
 }
 
@@ -179,7 +178,7 @@ extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int c
   int st = validate(problems, count, M, bits, group_size, Ns);
   if (st) return st;
   const long K = problems[0].K;
-  const Plan p = make_plan(Ns, count, K, M);
+  const Plan p = make_plan(Ns, count, K, M, bits);
   if (p.S == 0)
     return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld needs more than %zu split-K counters", (long long)M, kMaxCounters);
   const size_t need = p.ctr_bytes + p.part_bytes;

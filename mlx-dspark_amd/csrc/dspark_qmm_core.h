@@ -1,12 +1,6 @@
-// Inner loop of the small-M affine qmm shared by the dense kernel (dspark_qmm.hip) and the
-// grouped expert kernels (dspark_moe.hip).
-//
-// One wave accumulates, for NT tiles of 16 output features and one 16-row tile of x, the
-// partial sums over quantization groups [g0, g1):
-//     acc[j][r] (lane l) = y[row 4*(l>>4) + r][feature 16*j + (l & 15)]  (partial over groups)
-// Per group (64 k): the x fragment (A operand, 2 x 16 bytes per lane) is loaded once and
-// reused for the NT weight fragments; sum_k x (or -128 * sum_k x for 4-bit, see below) is one
-// MFMA pair against a constant operand and reused too.
+// Dequantization pieces of the small-M affine qmm shared by the dense split-K kernel
+// (dspark_qmm_splitk.h) and the expert kernels (dspark_moe.hip, dspark_moe_sk.h): packed
+// fields -> exact bf16 MFMA operands, and the matching order of the x fragments.
 #pragma once
 
 #include "dspark_common.h"
@@ -47,72 +41,6 @@ template <>
 struct WFrag<8> {
   u32x4_t v;
 };
-
-// Pointers one lane reads, already offset to its own row and quarter:
-//   xr    = x row (clamped to a valid row) + 16*q     (bf16)
-//   wr[j] = packed row n_j + (BITS == 4 ? 2*q : 4*q)  (words)
-//   sr[j], br[j] = scales / biases row n_j            (bf16)
-template <int BITS, int NT, int CH>
-__device__ __forceinline__ void qmm_wave_partial(const u16* __restrict__ xr, const u32* const (&wr)[NT],
-                                                 const u16* const (&sr)[NT], const u16* const (&br)[NT], int g0,
-                                                 int g1, f32x4_t (&acc)[NT]) {
-  // constant B operand that turns an MFMA into a row sum: -128 (4-bit offset) or 1.0
-  constexpr u32 kconst = (BITS == 4) ? 0xC300C300u : 0x3F803F80u;
-  const u32x4_t kb = {kconst, kconst, kconst, kconst};
-  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-
-  for (int gc = g0; gc < g1; gc += CH) {
-    u32x4_t xa[CH][2];
-    WFrag<BITS> wf[CH][NT];
-    u32 sv[CH][NT], bv[CH][NT];
-    // loads: unconditional (clamped group index) so the wait counts stay static
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int g = min(gc + i, g1 - 1);
-      xa[i][0] = ldg128(xr + 64 * g);
-      xa[i][1] = ldg128(xr + 64 * g + 8);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if constexpr (BITS == 4)
-          wf[i][j].v = ldg64(wr[j] + 8 * g);
-        else
-          wf[i][j].v = ldg128(wr[j] + 16 * g);
-        sv[i][j] = sr[j][g];
-        bv[i][j] = br[j][g];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      if (gc + i < g1) {
-        u32x4_t a0 = xa[i][0], a1 = xa[i][1];
-        if constexpr (BITS == 4) {
-          a0 = perm_x_u4(a0);
-          a1 = perm_x_u4(a1);
-        }
-        // 4-bit: c = -128 * sum x seeds the product MFMA, cancelling the +128 field offset;
-        // 8-bit: c = sum x.  Either way the bias term is (bias * bias_mul) * c.
-        f32x4_t c = mfma16x16x32(a0, kb, zero);
-        c = mfma16x16x32(a1, kb, c);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          f32x4_t p;
-          if constexpr (BITS == 4) {
-            p = mfma16x16x32(a0, unpack_u4(wf[i][j].v.x), c);
-            p = mfma16x16x32(a1, unpack_u4(wf[i][j].v.y), p);
-          } else {
-            p = mfma16x16x32(a0, unpack_u8(wf[i][j].v.x, wf[i][j].v.y), zero);
-            p = mfma16x16x32(a1, unpack_u8(wf[i][j].v.z, wf[i][j].v.w), p);
-          }
-          const float s = bf2f(sv[i][j]);
-          const float b = bf2f(bv[i][j]) * bias_mul;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(b, c[r], __builtin_fmaf(s, p[r], acc[j][r]));
-        }
-      }
-    }
-  }
-}
 
 // Lane pointers for weight row n (clamped by the caller) and quarter q.
 template <int BITS>

@@ -59,6 +59,91 @@ __device__ __forceinline__ float sum_bf16x8(u32x4_t v) {
   return s;
 }
 
+// Groups [gs, ge) of K slice sl of S (G groups per row). 4-bit slices start on an even group
+// because their weights are read two groups per load (see WSlice).
+template <int BITS>
+__device__ __forceinline__ void slice_groups(int sl, int S, int G, int& gs, int& ge) {
+  if constexpr (BITS == 4) {
+    const int pairs = (G + 1) >> 1;
+    gs = 2 * ((sl * pairs) / S);
+    ge = min(2 * (((sl + 1) * pairs) / S), G);
+  } else {
+    gs = (sl * G) / S;
+    ge = ((sl + 1) * G) / S;
+  }
+}
+
+// Kernel instantiation (8, 16 or 32 groups) that holds the largest of S slices of G groups,
+// as slice_groups() cuts them.
+inline int slice_capacity(long G, long S, int bits) {
+  const long per = bits == 4 ? 2 * (((G + 1) / 2 + S - 1) / S) : (G + S - 1) / S;
+  return per <= 8 ? 8 : per <= 16 ? 16 : 32;
+}
+
+// The weight fragments of one row over a K slice, loaded with 16-byte loads.
+//  8-bit: load gl = group gs+gl; lane quarter q holds bytes [16q, 16q+16), k [16q, 16q+16).
+//  4-bit: load j covers groups gs+2j and gs+2j+1 (64 bytes of the row): quarters 0,1 read
+//    bytes [16q, 16q+16) of the first group, quarters 2,3 bytes [16(q-2), ...) of the second,
+//    so one wave instruction reads 64 contiguous bytes of each of its 16 rows. frag_u4()
+//    swaps the halves between lanes l and l+32 (v_permlane32_swap), after which every lane
+//    holds 8 bytes of each group: bytes [8qs, 8qs+8), k [16qs, 16qs+16), qs = 2(q&1) + (q>>1).
+//  Loads past the slice repeat its last group (pair); their fragments are never used.
+template <int BITS, int KSMAX>
+struct WSlice {
+  static_assert(BITS == 8 || KSMAX % 2 == 0, "4-bit slices hold whole pairs");
+  u32x4_t v[BITS == 4 ? KSMAX / 2 : KSMAX];
+
+  // wrow: packed row (words); G: groups per row
+  __device__ __forceinline__ void load(const u32* wrow, int q, int gs, int gcount, int G) {
+    if constexpr (BITS == 4) {
+      const int pairs = (gcount + 1) >> 1;
+#pragma unroll
+      for (int j = 0; j < KSMAX / 2; ++j) {
+        const int g = gs + 2 * min(j, pairs - 1);
+        const int qq = (g + 1 < G) ? q : (q & 1);  // no second group at the row end: re-read the first
+        v[j] = ldg128(wrow + 8 * g + 4 * qq);
+      }
+    } else {
+#pragma unroll
+      for (int gl = 0; gl < KSMAX; ++gl) v[gl] = ldg128(wrow + 16 * (gs + min(gl, gcount - 1)) + 4 * q);
+    }
+  }
+};
+
+// (words of group 2j, words of group 2j+1) of 4-bit load j, each {k 16qs..+7, k 16qs+8..+15}
+__device__ __forceinline__ void frag_u4(u32x4_t v, u32x2_t& f0, u32x2_t& f1) {
+  const auto r0 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+  f0 = u32x2_t{r0[0], r1[0]};
+  f1 = u32x2_t{r0[1], r1[1]};
+}
+
+// lane quarter q's k offset inside a group: 16q (8-bit), 16qs (4-bit, after frag_u4)
+template <int BITS>
+__device__ __forceinline__ int k_quarter(int q) {
+  return BITS == 4 ? 16 * (2 * (q & 1) + (q >> 1)) : 16 * q;
+}
+
+// One group's contribution to a lane's 4 outputs: acc += s * (x . q) + b * sum x, with the
+// x fragments a0/a1 (from LDS) and c = the row sums (4-bit: -128 * sum x, the MFMA seed).
+template <int BITS>
+__device__ __forceinline__ void group_fma(u32x4_t a0, u32x4_t a1, f32x4_t c, u32x4_t w8, u32x2_t w4, float sf,
+                                          float bfv, f32x4_t& acc) {
+  f32x4_t p;
+  if constexpr (BITS == 4) {
+    p = mfma16x16x32(a0, unpack_u4(w4.x), c);
+    p = mfma16x16x32(a1, unpack_u4(w4.y), p);
+  } else {
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    p = mfma16x16x32(a0, unpack_u8(w8.x, w8.y), zero);
+    p = mfma16x16x32(a1, unpack_u8(w8.z, w8.w), p);
+  }
+  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
+  const float bm = bfv * bias_mul;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bm, c[r], __builtin_fmaf(sf, p[r], acc[r]));
+}
+
 template <int BITS, int NS, int KSMAX, bool SBVEC>
 __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   constexpr int XP = KSMAX * 64 + 8;  // LDS row pitch of the staged x slice (elements)
@@ -79,7 +164,9 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   const int sl = blockIdx.y;
   const int mt = blockIdx.z;
   const int G = K >> 6;
-  const int gs = (sl * G) / S, ge = ((sl + 1) * G) / S, gcount = ge - gs;
+  int gs, ge;
+  slice_groups<BITS>(sl, S, G, gs, ge);
+  const int gcount = ge - gs;
   const int m_base = mt * 16;
   const int m_rows = min(16, args.M - m_base);
 
@@ -108,17 +195,9 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
       xv[i] = ldg128(xb + (long)src * P.ldx + 8 * col);
     }
   }
-  // ---- 2. every weight fragment of this lane's row in the slice (clamped, unconditional)
-  WFrag<BITS> wf[KSMAX];
-  const u32* wr = wrow_ptr<BITS>(P.w, n, K, q);
-#pragma unroll
-  for (int gl = 0; gl < KSMAX; ++gl) {
-    const int g = gs + min(gl, gcount - 1);
-    if constexpr (BITS == 4)
-      wf[gl].v = ldg64(wr + 8 * g);
-    else
-      wf[gl].v = ldg128(wr + 16 * g);
-  }
+  // ---- 2. every weight load of this lane's row in the slice (clamped, unconditional)
+  WSlice<BITS, KSMAX> wsl;
+  wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
   // ---- 3. scales / biases of the row's groups in the slice
   constexpr int SBV = (KSMAX + 7) / 8;
   u32x4_t svv[SBV], bvv[SBV];
@@ -169,25 +248,17 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   __syncthreads();
 
   // ---- 5. MFMA loop over the slice
-  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4_t acc = zero;
-  const u16* xl = &xs[c16 * XP + 16 * q];
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const u16* xl = &xs[c16 * XP + k_quarter<BITS>(q)];
+  u32x2_t w4[2] = {};
 #pragma unroll
   for (int gl = 0; gl < KSMAX; ++gl) {
     if (gl < gcount) {
+      if (BITS == 4 && (gl & 1) == 0) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
       const u32x4_t a0 = lds128(xl + 64 * gl), a1 = lds128(xl + 64 * gl + 8);
       // rows 4q..4q+3. (Read as a float vector: bit-casting ext-vector elements one by one
       // miscompiles to a single-dword read.)
       const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[gl * 16 + 4 * q]);
-      f32x4_t p;
-      if constexpr (BITS == 4) {
-        p = mfma16x16x32(a0, unpack_u4(wf[gl].v.x), c);  // seeded with -128 * sum x
-        p = mfma16x16x32(a1, unpack_u4(wf[gl].v.y), p);
-      } else {
-        p = mfma16x16x32(a0, unpack_u8(wf[gl].v.x, wf[gl].v.y), zero);
-        p = mfma16x16x32(a1, unpack_u8(wf[gl].v.z, wf[gl].v.w), p);
-      }
       u32 sbits, bbits;
       if constexpr (SBVEC) {
         sbits = bf_field(svv[gl >> 3], gl & 7);
@@ -196,9 +267,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
         sbits = svs[gl];
         bbits = bvs[gl];
       }
-      const float sf = bf2f(sbits), bf = bf2f(bbits) * bias_mul;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bf, c[r], __builtin_fmaf(sf, p[r], acc[r]));
+      group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : gl], w4[gl & 1], bf2f(sbits), bf2f(bbits), acc);
     }
   }
 
@@ -250,103 +319,6 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v);
   }
   if (tid == 0) __hip_atomic_store(&P.ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-}  // namespace dspark
-
-namespace dspark {
-
-// Intra-workgroup split-K variant for small N (few 16-row tiles): workgroup = W waves = one
-// 16-row output tile; wave w takes groups [w*G/W, (w+1)*G/W) (at most KSW) and issues all of
-// its weight, x and scale/bias loads up front; the W partial tiles are summed in LDS in wave
-// order. No cross-workgroup exchange, so the critical path is one memory round trip.
-// x fragments come straight from global memory (L2-resident), the group sums of x from an
-// MFMA against a constant operand.
-template <int BITS, int W, int KSW>
-__global__ __launch_bounds__(64 * W) void qmm_ws_kernel(const QmmSkArgs args) {
-  __shared__ float red[W][256];
-  const int bx = blockIdx.x;
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < kQmmMaxProblems; ++i)
-    if (i < args.count && bx >= args.p[i].strip0) pi = i;
-  const QmmSkProb& P = args.p[pi];
-  const int N = P.N, K = P.K;
-  const int tile = bx - P.strip0;  // 16-row tile
-  const int mt = blockIdx.z;
-  const int G = K >> 6;
-  const int m_base = mt * 16;
-  const int m_rows = min(16, args.M - m_base);
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int c16 = lane & 15, q = lane >> 4;
-  const int g0 = (wave * G) / W, g1 = ((wave + 1) * G) / W, gcount = g1 - g0;
-  const int ncol = tile * 16 + c16;
-  const int n = min(ncol, N - 1);
-
-  WFrag<BITS> wf[KSW];
-  u32x4_t xa[KSW][2];
-  u32 sv[KSW], bv[KSW];
-  const u32* wr = wrow_ptr<BITS>(P.w, n, K, q);
-  const u16* xr = P.x + (long)(m_base + min(c16, m_rows - 1)) * P.ldx + 16 * q;
-  const u16* srow = P.s + (long)n * G;
-  const u16* brow = P.b + (long)n * G;
-  if (gcount > 0) {
-#pragma unroll
-    for (int i = 0; i < KSW; ++i) {
-      const int g = g0 + min(i, gcount - 1);
-      if constexpr (BITS == 4)
-        wf[i].v = ldg64(wr + 8 * g);
-      else
-        wf[i].v = ldg128(wr + 16 * g);
-    }
-#pragma unroll
-    for (int i = 0; i < KSW; ++i) {
-      const int g = g0 + min(i, gcount - 1);
-      xa[i][0] = ldg128(xr + 64 * g);
-      xa[i][1] = ldg128(xr + 64 * g + 8);
-      sv[i] = srow[g];
-      bv[i] = brow[g];
-    }
-  }
-  constexpr u32 kconst = (BITS == 4) ? 0xC300C300u : 0x3F803F80u;
-  const u32x4_t kb = {kconst, kconst, kconst, kconst};
-  constexpr float bias_mul = (BITS == 4) ? (-1.0f / 128.0f) : 1.0f;
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4_t acc = zero;
-#pragma unroll
-  for (int i = 0; i < KSW; ++i) {
-    if (i < gcount) {
-      u32x4_t a0 = xa[i][0], a1 = xa[i][1];
-      if constexpr (BITS == 4) {
-        a0 = perm_x_u4(a0);
-        a1 = perm_x_u4(a1);
-      }
-      f32x4_t c = mfma16x16x32(a0, kb, zero);
-      c = mfma16x16x32(a1, kb, c);
-      f32x4_t p;
-      if constexpr (BITS == 4) {
-        p = mfma16x16x32(a0, unpack_u4(wf[i].v.x), c);
-        p = mfma16x16x32(a1, unpack_u4(wf[i].v.y), p);
-      } else {
-        p = mfma16x16x32(a0, unpack_u8(wf[i].v.x, wf[i].v.y), zero);
-        p = mfma16x16x32(a1, unpack_u8(wf[i].v.z, wf[i].v.w), p);
-      }
-      const float sf = bf2f(sv[i]), bf = bf2f(bv[i]) * bias_mul;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bf, c[r], __builtin_fmaf(sf, p[r], acc[r]));
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) red[wave][(4 * q + r) * 16 + c16] = acc[r];
-  __syncthreads();
-  if (tid < 256) {
-    float v = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < W; ++ww) v += red[ww][tid];
-    const int m = tid >> 4, nc = tile * 16 + (tid & 15);
-    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v);
-  }
 }
 
 }  // namespace dspark
