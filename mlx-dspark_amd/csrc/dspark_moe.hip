@@ -16,6 +16,7 @@
 // (counting sort, stable in pair id). The grouped qmm launches one workgroup per
 // (expert, 16-feature tile); workgroups of unselected experts exit at once, every selected
 // expert's weight tile is streamed once for all of its tokens (<= 16 at verify widths).
+#include "dspark_moe_rc.h"
 #include "dspark_moe_sk.h"
 
 namespace dspark {
@@ -441,6 +442,72 @@ MoeWorkspace moe_layout(long M, long H, long I, long E, long k, int bits) {
   return w;
 }
 
+MoeRcArgs rc_args(const MoeSkArgs& a) {
+  MoeRcArgs r{};
+  r.x = a.x;
+  r.row_index = a.row_index;
+  r.offsets = a.offsets;
+  r.w0 = a.w0;
+  r.s0 = a.s0;
+  r.b0 = a.b0;
+  r.w1 = a.w1;
+  r.s1 = a.s1;
+  r.b1 = a.b1;
+  r.y = a.y;
+  r.ldx = a.ldx;
+  r.ldy = a.ldy;
+  r.K = a.K;
+  r.N = a.N;
+  r.row_div = a.row_div;
+  r.P_max = a.P_max;
+  r.mtiles = a.mtiles;
+  return r;
+}
+
+// Small-bucket plan (moe_rc_kernel): K parts per workgroup and groups per part, or kw = 0
+// when the whole-K workgroup does not apply (the split-K kernel then runs).
+struct RcPlan {
+  int kw, ksmax, strips;
+};
+
+RcPlan rc_plan(long K, long N, bool swiglu, const void* s, const void* b) {
+  RcPlan p{};
+  const long G = K / 64;
+  if (K % 128 || !aligned(s, 4) || !aligned(b, 4)) return p;
+  const int kws[3] = {1, 2, 4};
+  for (int cap : {16, 32}) {
+    for (int kw : kws) {
+      if (swiglu && kw == 4) break;
+      const long per = 2 * ((G / 2 + kw - 1) / kw);
+      if (per <= cap) {
+        p.kw = kw;
+        p.ksmax = cap;
+        const long cols = swiglu ? 8 * (4 / kw) : 16 * (4 / kw);  // output columns per workgroup
+        p.strips = (int)((N + cols - 1) / cols);
+        return p;
+      }
+    }
+  }
+  return p;
+}
+
+template <bool SWIGLU>
+int launch_moe_rc(const MoeRcArgs& a, const RcPlan& p, int E, int bits, hipStream_t s) {
+  const dim3 grid((unsigned)p.strips, (unsigned)(E * a.mtiles));
+#define MOE_RC(B, KS, KW) hipLaunchKernelGGL((moe_rc_kernel<B, KS, KW, SWIGLU>), grid, dim3(256), 0, s, a)
+#define MOE_RC_KW(B, KS)                                     \
+  if (p.kw == 1) MOE_RC(B, KS, 1);                           \
+  else if (SWIGLU || p.kw == 2) MOE_RC(B, KS, 2);            \
+  else MOE_RC(B, KS, (SWIGLU ? 2 : 4));
+#define MOE_RC_BITS(B) \
+  if (p.ksmax == 16) { MOE_RC_KW(B, 16) } else { MOE_RC_KW(B, 32) }
+  if (bits == 4) { MOE_RC_BITS(4) } else { MOE_RC_BITS(8) }
+#undef MOE_RC_BITS
+#undef MOE_RC_KW
+#undef MOE_RC
+  return check_launch(SWIGLU ? "moe gate/up" : "moe down");
+}
+
 template <bool SWIGLU>
 int launch_moe_sk(const MoeSkArgs& a, const MoePlan& p, int E, int bits, hipStream_t s) {
   const dim3 grid((unsigned)p.strips, (unsigned)p.S, (unsigned)(E * p.mtiles));
@@ -586,7 +653,12 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   g.strips = L.gu.strips;
   g.mtiles = L.gu.mtiles;
   g.S = L.gu.S;
-  if ((st = launch_moe_sk<true>(g, L.gu, (int)E, bits, s))) return st;
+  const RcPlan rgu = rc_plan(H, I, true, s_gate, b_gate), rgu2 = rc_plan(H, I, true, s_up, b_up);
+  if (rgu.kw && rgu2.kw) {
+    if ((st = launch_moe_rc<true>(rc_args(g), rgu, (int)E, bits, s))) return st;
+  } else if ((st = launch_moe_sk<true>(g, L.gu, (int)E, bits, s))) {
+    return st;
+  }
 
   MoeSkArgs d{};
   d.x = h;
@@ -607,7 +679,12 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   d.strips = L.dn.strips;
   d.mtiles = L.dn.mtiles;
   d.S = L.dn.S;
-  if ((st = launch_moe_sk<false>(d, L.dn, (int)E, bits, s))) return st;
+  const RcPlan rdn = rc_plan(I, H, false, s_down, b_down);
+  if (rdn.kw) {
+    if ((st = launch_moe_rc<false>(rc_args(d), rdn, (int)E, bits, s))) return st;
+  } else if ((st = launch_moe_sk<false>(d, L.dn, (int)E, bits, s))) {
+    return st;
+  }
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)M, (unsigned)((H + 255) / 256)), dim3(256), 0, s, ypair, pos,
                      scores_ws, static_cast<u16*>(out), (int)H, (int)k);

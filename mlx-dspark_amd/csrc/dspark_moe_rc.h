@@ -1,0 +1,193 @@
+// Grouped expert qmm for small buckets (gfx950): the fused MoE block's projections when each
+// expert sees a few rows (the verify regime: M <= 16 tokens, top-k of many experts, so a
+// bucket holds ~M*k/E rows).
+//
+// Workgroup = 4 waves = one expert x one strip of output columns x the whole K, so no
+// partial sums leave the workgroup. Wave w takes column tile w % NT and K part w / NT (KW
+// parts, NT = 4 / KW tiles); the KW partial tiles are summed in LDS in part order. SwiGLU mode:
+// even tiles read gate rows, odd tiles the up rows of the same 16 columns, and the strip's
+// reduced tiles become h = swiglu(gate, up).
+// The bucket's rows go through the MFMA in passes of RC = 4: x rows are gathered into LDS
+// (4 rows x K, with their per-group sums) and MFMA A rows 4..15 repeat row 3; their outputs
+// are dropped. One pass covers buckets of up to 4 rows; larger tiles loop, reusing the
+// weights held in registers.
+// Issue order of a workgroup: bucket bounds -> x row indices (pass 0) -> every weight,
+// scale and bias load -> x loads (waiting only for the row indices, which were issued first)
+// -> LDS staging -> MFMA -> LDS reduction -> output.
+#pragma once
+
+#include "dspark_qmm_splitk.h"
+
+namespace dspark {
+
+struct MoeRcArgs {
+  const u16* x;          // [rows, K] activations
+  const int* row_index;  // nullable: x row of bucket position p is row_index[p] / row_div
+  const int* offsets;    // [E + 1] bucket starts (sorted pair positions)
+  const u32* w0;         // [E, N, K*bits/32] plain / gate
+  const u16* s0;
+  const u16* b0;
+  const u32* w1;         // up (SwiGLU)
+  const u16* s1;
+  const u16* b1;
+  u16* y;                // [P, N] bf16
+  long ldx, ldy;
+  int K, N, row_div, P_max, mtiles;
+};
+
+// Requires K % 128 == 0, K <= KW * KSMAX * 64, 4-byte aligned scales and biases.
+template <int BITS, int KSMAX, int KW, bool SWIGLU>
+__global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_rc_kernel(const MoeRcArgs a) {
+  constexpr int NT = 4 / KW;  // 16-column tiles per workgroup
+  static_assert(KW == 1 || KW == 2 || KW == 4, "K parts");
+  static_assert(!SWIGLU || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
+  constexpr int RC = 4;                    // bucket rows per pass
+  constexpr int KMAX = KW * KSMAX * 64;    // x elements per row
+  constexpr int XP = KMAX + 8;             // LDS row pitch (elements): rows 16 bytes apart in banks
+  constexpr int XCH = RC * KMAX / 8 / 256; // 16-byte x chunks per thread per pass
+  static_assert(XCH >= 1 && (RC * KMAX / 8) % 256 == 0, "x staging shape");
+  __shared__ __attribute__((aligned(16))) u16 xs[RC * XP];
+  __shared__ __attribute__((aligned(16))) float xsum[KW * KSMAX][RC];  // 4-bit: -128 * sum x
+  __shared__ float red[4][RC * 16];
+
+  const int strip = blockIdx.x;
+  const int e = blockIdx.y / a.mtiles, mt = blockIdx.y - e * a.mtiles;
+  const int p0 = a.offsets[e] + 16 * mt;
+  const int p1 = min(a.offsets[e + 1], a.P_max);
+  if (p0 >= p1) return;
+  const int m_rows = min(16, p1 - p0);
+  const int K = a.K, N = a.N, G = K >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int tile = wave % NT, kp = wave / NT;
+  // K parts start on even groups (G is even): weights of 4-bit rows and the scale/bias
+  // pairs are read two groups at a time
+  int gs, ge;
+  slice_groups<4>(kp, KW, G, gs, ge);
+  const int gcount = ge - gs;
+  const bool up = SWIGLU && (tile & 1);
+  const int ncol = SWIGLU ? strip * (8 * NT) + 16 * (tile >> 1) + c16 : strip * (16 * NT) + 16 * tile + c16;
+  const int n = min(ncol, N - 1);
+  const long wstride = (long)N * (K * BITS / 32), sstride = (long)N * G;
+  const u32* wmat = (up ? a.w1 : a.w0) + e * wstride;
+  const u16* smat = (up ? a.s1 : a.s0) + e * sstride;
+  const u16* bmat = (up ? a.b1 : a.b0) + e * sstride;
+
+  // x chunk i of this thread: row r (of the pass), column chunk col (8 elements)
+  const int cpr = K >> 3;
+  const int xtotal = RC * cpr;
+  int xrow[XCH], xcol[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = min(tid + 256 * i, xtotal - 1);
+    xrow[i] = c / cpr;
+    xcol[i] = c - xrow[i] * cpr;
+  }
+  auto src_row = [&](int r0, int r) {
+    const int pr = p0 + min(r0 + r, m_rows - 1);
+    return (a.row_index ? a.row_index[pr] : pr) / a.row_div;
+  };
+  // ---- 1. x row indices of pass 0
+  int src[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) src[i] = src_row(0, xrow[i]);
+  // ---- 2. weights, scales, biases of this wave's rows and K part
+  WSlice<BITS, KSMAX> wsl;
+  wsl.load(wmat + (long)n * (K * BITS / 32), q, gs, gcount, G);
+  u32 svp[KSMAX / 2], bvp[KSMAX / 2];  // bf16 pairs (group 2j low, 2j+1 high)
+  const u32* srow = reinterpret_cast<const u32*>(smat + (long)n * G + gs);
+  const u32* brow = reinterpret_cast<const u32*>(bmat + (long)n * G + gs);
+#pragma unroll
+  for (int j = 0; j < KSMAX / 2; ++j) {
+    const int jj = min(j, (gcount >> 1) - 1);
+    svp[j] = srow[jj];
+    bvp[j] = brow[jj];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4_t acc;
+  for (int r0 = 0; r0 < m_rows; r0 += RC) {
+    const int rows = min(RC, m_rows - r0);
+    if (r0 > 0) {
+#pragma unroll
+      for (int i = 0; i < XCH; ++i) src[i] = src_row(r0, xrow[i]);
+      __syncthreads();  // the previous pass has finished with xs, xsum and red
+    }
+    // ---- 3. x rows of the pass -> LDS with their per-group sums (8 lanes per (row, group))
+    u32x4_t xv[XCH];
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const bool valid = tid + 256 * i < xtotal;
+      u32x4_t v = xv[i];
+      float s8 = sum_bf16x8(v);
+      s8 += shfl_xor(s8, 1);
+      s8 += shfl_xor(s8, 2);
+      s8 += shfl_xor(s8, 4);
+      if (BITS == 4) {
+        v = perm_x_u4(v);
+        s8 *= -128.0f;
+      }
+      if (valid) {
+        *reinterpret_cast<u32x4_t*>(&xs[xrow[i] * XP + 8 * xcol[i]]) = v;
+        if ((xcol[i] & 7) == 0) xsum[xcol[i] >> 3][xrow[i]] = s8;
+      }
+    }
+    __syncthreads();
+    // ---- 4. MFMA over the wave's groups (A rows >= RC repeat row RC-1). The empty asm makes
+    // the weight registers opaque per pass, so the compiler cannot hoist the dequantized
+    // fragments of every group out of the pass loop (they would need 8 registers per group).
+#pragma unroll
+    for (int j = 0; j < (BITS == 4 ? KSMAX / 2 : KSMAX); ++j) asm volatile("" : "+v"(wsl.v[j]));
+    acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const u16* xl = &xs[min(c16, RC - 1) * XP + k_quarter<BITS>(q)];
+    u32x2_t w4[2] = {};
+#pragma unroll
+    for (int gl = 0; gl < KSMAX; ++gl) {
+      if (gl < gcount) {
+        if (BITS == 4 && (gl & 1) == 0) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
+        const int g = gs + gl;
+        const u32x4_t a0 = lds128(xl + 64 * g), a1 = lds128(xl + 64 * g + 8);
+        const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[g][0]);
+        const u32 sb = (gl & 1) ? (svp[gl >> 1] >> 16) : (svp[gl >> 1] & 0xFFFFu);
+        const u32 bb = (gl & 1) ? (bvp[gl >> 1] >> 16) : (bvp[gl >> 1] & 0xFFFFu);
+        group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : gl], w4[gl & 1], bf2f(sb), bf2f(bb), acc);
+      }
+    }
+    // ---- 5. partial tiles (rows 0..RC-1 live in lanes q == 0) -> LDS, summed in part order
+    if (q == 0) {
+#pragma unroll
+      for (int r = 0; r < RC; ++r) red[wave][r * 16 + c16] = acc[r];
+    }
+    __syncthreads();
+    constexpr int OUT_TILES = SWIGLU ? NT / 2 : NT;
+    if (tid < OUT_TILES * RC * 16) {
+      const int ot = tid / (RC * 16), el = tid - ot * (RC * 16);
+      const int r = el >> 4, cc = el & 15;
+      float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+      for (int k2 = 0; k2 < KW; ++k2) {
+        if constexpr (SWIGLU) {
+          v0 += red[k2 * NT + 2 * ot][el];
+          v1 += red[k2 * NT + 2 * ot + 1][el];
+        } else {
+          v0 += red[k2 * NT + ot][el];
+        }
+      }
+      const int col = strip * (16 * OUT_TILES) + 16 * ot + cc;
+      if (r < rows && col < N) {
+        float out = v0;
+        if constexpr (SWIGLU) {
+          // h = silu(gate) * up with the bf16 rounding of each elementwise op
+          const float g = bf2f(f2bf(v0)), u = bf2f(f2bf(v1));
+          const float sg = bf2f(f2bf(1.0f / (1.0f + expf(-g))));
+          out = bf2f(f2bf(g * sg)) * u;
+        }
+        a.y[(long)(p0 + r0 + r) * a.ldy + col] = f2bf(out);
+      }
+    }
+  }
+}
+
+}  // namespace dspark
