@@ -473,7 +473,7 @@ struct RcPlan {
 RcPlan rc_plan(long K, long N, bool swiglu, const void* s, const void* b) {
   RcPlan p{};
   const long G = K / 64;
-  if (K % 128 || !aligned(s, 4) || !aligned(b, 4)) return p;
+  if (K % 128 || (N * G) % 8 || !aligned(s, 16) || !aligned(b, 16)) return p;
   const int kws[3] = {1, 2, 4};
   for (int cap : {16, 32}) {
     for (int kw : kws) {

@@ -11,8 +11,9 @@
 // (4 rows x K, with their per-group sums) and MFMA A rows 4..15 repeat row 3; their outputs
 // are dropped. One pass covers buckets of up to 4 rows; larger tiles loop, reusing the
 // weights held in registers.
-// Issue order of a workgroup: bucket bounds -> x row indices (pass 0) -> every weight,
-// scale and bias load -> x loads (waiting only for the row indices, which were issued first)
+// Issue order of a workgroup: bucket bounds -> x row indices (pass 0) -> every weight load
+// -> the tiles' scale and bias rows (contiguous 16-byte chunks, one or two per thread, kept in
+// LDS) -> x loads (waiting only for the row indices, which were issued first)
 // -> LDS staging -> MFMA -> LDS reduction -> output.
 #pragma once
 
@@ -35,7 +36,8 @@ struct MoeRcArgs {
   int K, N, row_div, P_max, mtiles;
 };
 
-// Requires K % 128 == 0, K <= KW * KSMAX * 64, 4-byte aligned scales and biases.
+// Requires K % 128 == 0, K <= KW * KSMAX * 64, N * K / 64 % 8 == 0 and 16-byte aligned scales
+// and biases.
 template <int BITS, int KSMAX, int KW, bool SWIGLU>
 __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_rc_kernel(const MoeRcArgs a) {
   constexpr int NT = 4 / KW;  // 16-column tiles per workgroup
@@ -49,6 +51,10 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
   __shared__ __attribute__((aligned(16))) u16 xs[RC * XP];
   __shared__ __attribute__((aligned(16))) float xsum[KW * KSMAX][RC];  // 4-bit: -128 * sum x
   __shared__ float red[4][RC * 16];
+  // scales (array 0) and biases (array 1) of each tile's 16 rows, all groups, as stored:
+  // row r of tile t at [t][r * G + g]
+  constexpr int GMAX = KW * KSMAX;
+  __shared__ __attribute__((aligned(16))) u16 sbl[2][NT][16 * GMAX];
 
   const int strip = blockIdx.x;
   const int e = blockIdx.y / a.mtiles, mt = blockIdx.y - e * a.mtiles;
@@ -94,14 +100,20 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
   // ---- 2. weights, scales, biases of this wave's rows and K part
   WSlice<BITS, KSMAX> wsl;
   wsl.load(wmat + (long)n * (K * BITS / 32), q, gs, gcount, G);
-  u32 svp[KSMAX / 2], bvp[KSMAX / 2];  // bf16 pairs (group 2j low, 2j+1 high)
-  const u32* srow = reinterpret_cast<const u32*>(smat + (long)n * G + gs);
-  const u32* brow = reinterpret_cast<const u32*>(bmat + (long)n * G + gs);
+  // scale / bias blocks of the workgroup's tiles: 16 rows x G contiguous bf16 per (array,
+  // tile), read in 16-byte chunks (2G per block; the last strip's block stops at the matrix end)
+  constexpr int SBCH = (4 * NT * GMAX + 255) / 256;
+  const int nblk = 2 * G;
+  u32x4_t sbv[SBCH];
 #pragma unroll
-  for (int j = 0; j < KSMAX / 2; ++j) {
-    const int jj = min(j, (gcount >> 1) - 1);
-    svp[j] = srow[jj];
-    bvp[j] = brow[jj];
+  for (int j = 0; j < SBCH; ++j) {
+    const int ci = min(tid + 256 * j, 2 * NT * nblk - 1);
+    const int arr = ci / (NT * nblk), t = (ci / nblk) % NT, cc = ci % nblk;
+    const bool tup = SWIGLU && (t & 1);
+    const int n0 = SWIGLU ? strip * (8 * NT) + 16 * (t >> 1) : strip * (16 * NT) + 16 * t;
+    const u16* base = arr == 0 ? (tup ? a.s1 : a.s0) : (tup ? a.b1 : a.b0);
+    const long off = min((long)n0 * G + 8 * cc, (long)N * G - 8);  // in bounds of expert e's block
+    sbv[j] = ldg128(base + e * sstride + off);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -134,6 +146,16 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
         if ((xcol[i] & 7) == 0) xsum[xcol[i] >> 3][xrow[i]] = s8;
       }
     }
+    if (r0 == 0) {
+#pragma unroll
+      for (int j = 0; j < SBCH; ++j) {
+        const int ci = tid + 256 * j;
+        if (ci < 2 * NT * nblk) {
+          const int arr = ci / (NT * nblk), t = (ci / nblk) % NT, cc = ci % nblk;
+          *reinterpret_cast<u32x4_t*>(&sbl[arr][t][8 * cc]) = sbv[j];
+        }
+      }
+    }
     __syncthreads();
     // ---- 4. MFMA over the wave's groups (A rows >= RC repeat row RC-1). The empty asm makes
     // the weight registers opaque per pass, so the compiler cannot hoist the dequantized
@@ -142,7 +164,11 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
     for (int j = 0; j < (BITS == 4 ? KSMAX / 2 : KSMAX); ++j) asm volatile("" : "+v"(wsl.v[j]));
     acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const u16* xl = &xs[min(c16, RC - 1) * XP + k_quarter<BITS>(q)];
+    const int nrow = max(n - (ncol - c16), 0);  // this lane's row in its tile block (0 past N)
+    const u32* sp = reinterpret_cast<const u32*>(&sbl[0][tile][nrow * G + gs]);
+    const u32* bp = reinterpret_cast<const u32*>(&sbl[1][tile][nrow * G + gs]);
     u32x2_t w4[2] = {};
+    u32 sp2 = 0, bp2 = 0;
 #pragma unroll
     for (int gl = 0; gl < KSMAX; ++gl) {
       if (gl < gcount) {
@@ -150,8 +176,12 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
         const int g = gs + gl;
         const u32x4_t a0 = lds128(xl + 64 * g), a1 = lds128(xl + 64 * g + 8);
         const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[g][0]);
-        const u32 sb = (gl & 1) ? (svp[gl >> 1] >> 16) : (svp[gl >> 1] & 0xFFFFu);
-        const u32 bb = (gl & 1) ? (bvp[gl >> 1] >> 16) : (bvp[gl >> 1] & 0xFFFFu);
+        if ((gl & 1) == 0) {
+          sp2 = sp[gl >> 1];
+          bp2 = bp[gl >> 1];
+        }
+        const u32 sb = (gl & 1) ? (sp2 >> 16) : (sp2 & 0xFFFFu);
+        const u32 bb = (gl & 1) ? (bp2 >> 16) : (bp2 & 0xFFFFu);
         group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : gl], w4[gl & 1], bf2f(sb), bf2f(bb), acc);
       }
     }
