@@ -55,6 +55,31 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
       float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
 }
 
+// Sum over each aligned group of 8 lanes, returned to all 8: the butterfly over lane bits 0,
+// 1, 2 (v + v^1, then + v^2, then + v^4) with DPP exchanges (quad permutes, half-row mirror:
+// lane i of an 8-lane group pairs with 7 - i, which holds the other quad's sum).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm 1,0,3,2
+  v += dpp_mov<0x4E>(v);   // quad_perm 2,3,0,1
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  return v;
+}
+
+// (v & m) | o as one v_and_or_b32 (the mask in an SGPR, o in a VGPR): the compiler splits it
+// into two instructions when both constants are literals.
+__device__ __forceinline__ u32 and_or(u32 v, u32 m, u32 o) {
+  u32 d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(v), "s"(m), "v"(o));
+  return d;
+}
+
+// Wave-uniform copy of a value the compiler cannot prove uniform (e.g. threadIdx.x >> 6).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // ---------------------------------------------------------------- host helpers
 
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));

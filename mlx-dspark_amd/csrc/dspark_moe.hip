@@ -474,6 +474,8 @@ RcPlan rc_plan(long K, long N, bool swiglu, const void* s, const void* b) {
   RcPlan p{};
   const long G = K / 64;
   if (K % 128 || (N * G) % 8 || !aligned(s, 16) || !aligned(b, 16)) return p;
+  // fewest K parts whose largest part has <= 16 groups, else <= 32; the kernel instance is
+  // the smallest of 8, 12, 16, 24, 32 groups that holds the part
   const int kws[3] = {1, 2, 4};
   for (int cap : {16, 32}) {
     for (int kw : kws) {
@@ -481,7 +483,7 @@ RcPlan rc_plan(long K, long N, bool swiglu, const void* s, const void* b) {
       const long per = 2 * ((G / 2 + kw - 1) / kw);
       if (per <= cap) {
         p.kw = kw;
-        p.ksmax = cap;
+        p.ksmax = per <= 8 ? 8 : per <= 12 ? 12 : per <= 16 ? 16 : per <= 24 ? 24 : 32;
         const long cols = swiglu ? 8 * (4 / kw) : 16 * (4 / kw);  // output columns per workgroup
         p.strips = (int)((N + cols - 1) / cols);
         return p;
@@ -499,8 +501,12 @@ int launch_moe_rc(const MoeRcArgs& a, const RcPlan& p, int E, int bits, hipStrea
   if (p.kw == 1) MOE_RC(B, KS, 1);                           \
   else if (SWIGLU || p.kw == 2) MOE_RC(B, KS, 2);            \
   else MOE_RC(B, KS, (SWIGLU ? 2 : 4));
-#define MOE_RC_BITS(B) \
-  if (p.ksmax == 16) { MOE_RC_KW(B, 16) } else { MOE_RC_KW(B, 32) }
+#define MOE_RC_BITS(B)                   \
+  if (p.ksmax == 8) { MOE_RC_KW(B, 8) }          \
+  else if (p.ksmax == 12) { MOE_RC_KW(B, 12) }   \
+  else if (p.ksmax == 16) { MOE_RC_KW(B, 16) }   \
+  else if (p.ksmax == 24) { MOE_RC_KW(B, 24) }   \
+  else { MOE_RC_KW(B, 32) }
   if (bits == 4) { MOE_RC_BITS(4) } else { MOE_RC_BITS(8) }
 #undef MOE_RC_BITS
 #undef MOE_RC_KW

@@ -37,23 +37,23 @@ struct MoeRcArgs {
 };
 
 // Requires K % 128 == 0, K <= KW * KSMAX * 64, N * K / 64 % 8 == 0 and 16-byte aligned scales
-// and biases.
+// and biases. KSMAX (even) is the largest K part in groups.
 template <int BITS, int KSMAX, int KW, bool SWIGLU>
-__global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_rc_kernel(const MoeRcArgs a) {
+__global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_rc_kernel(const MoeRcArgs a) {
   constexpr int NT = 4 / KW;  // 16-column tiles per workgroup
   static_assert(KW == 1 || KW == 2 || KW == 4, "K parts");
   static_assert(!SWIGLU || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
-  constexpr int RC = 4;                    // bucket rows per pass
-  constexpr int KMAX = KW * KSMAX * 64;    // x elements per row
-  constexpr int XP = KMAX + 8;             // LDS row pitch (elements): rows 16 bytes apart in banks
-  constexpr int XCH = RC * KMAX / 8 / 256; // 16-byte x chunks per thread per pass
-  static_assert(XCH >= 1 && (RC * KMAX / 8) % 256 == 0, "x staging shape");
+  static_assert(KSMAX % 2 == 0, "groups come in pairs");
+  constexpr int RC = 4;                              // bucket rows per pass
+  constexpr int KMAX = KW * KSMAX * 64;              // x elements per row
+  constexpr int XP = KMAX + 8;                       // LDS row pitch (elements): rows 16 bytes apart in banks
+  constexpr int XCH = (RC * KMAX / 8 + 255) / 256;   // 16-byte x chunks per thread per pass
+  constexpr int GMAX = KW * KSMAX;
   __shared__ __attribute__((aligned(16))) u16 xs[RC * XP];
-  __shared__ __attribute__((aligned(16))) float xsum[KW * KSMAX][RC];  // 4-bit: -128 * sum x
+  __shared__ __attribute__((aligned(16))) float xsum[GMAX][RC];  // 4-bit: -128 * sum x
   __shared__ float red[4][RC * 16];
   // scales (array 0) and biases (array 1) of each tile's 16 rows, all groups, as stored:
   // row r of tile t at [t][r * G + g]
-  constexpr int GMAX = KW * KSMAX;
   __shared__ __attribute__((aligned(16))) u16 sbl[2][NT][16 * GMAX];
 
   const int strip = blockIdx.x;
@@ -63,21 +63,19 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
   if (p0 >= p1) return;
   const int m_rows = min(16, p1 - p0);
   const int K = a.K, N = a.N, G = K >> 6;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int c16 = lane & 15, q = lane >> 4;
   const int tile = wave % NT, kp = wave / NT;
   // K parts start on even groups (G is even): weights of 4-bit rows and the scale/bias
   // pairs are read two groups at a time
   int gs, ge;
   slice_groups<4>(kp, KW, G, gs, ge);
-  const int gcount = ge - gs;
+  const int gcount = ge - gs;  // even, >= 2
   const bool up = SWIGLU && (tile & 1);
   const int ncol = SWIGLU ? strip * (8 * NT) + 16 * (tile >> 1) + c16 : strip * (16 * NT) + 16 * tile + c16;
   const int n = min(ncol, N - 1);
   const long wstride = (long)N * (K * BITS / 32), sstride = (long)N * G;
   const u32* wmat = (up ? a.w1 : a.w0) + e * wstride;
-  const u16* smat = (up ? a.s1 : a.s0) + e * sstride;
-  const u16* bmat = (up ? a.b1 : a.b0) + e * sstride;
 
   // x chunk i of this thread: row r (of the pass), column chunk col (8 elements)
   const int cpr = K >> 3;
@@ -97,11 +95,12 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
   int src[XCH];
 #pragma unroll
   for (int i = 0; i < XCH; ++i) src[i] = src_row(0, xrow[i]);
-  // ---- 2. weights, scales, biases of this wave's rows and K part
+  // ---- 2. weights of this wave's rows and K part
   WSlice<BITS, KSMAX> wsl;
   wsl.load(wmat + (long)n * (K * BITS / 32), q, gs, gcount, G);
-  // scale / bias blocks of the workgroup's tiles: 16 rows x G contiguous bf16 per (array,
-  // tile), read in 16-byte chunks (2G per block; the last strip's block stops at the matrix end)
+  // ---- 3. scale / bias blocks of the workgroup's tiles: 16 rows x G contiguous bf16 per
+  // (array, tile), read in 16-byte chunks (2G per block; the last strip's block stops at the
+  // matrix end)
   constexpr int SBCH = (4 * NT * GMAX + 255) / 256;
   const int nblk = 2 * G;
   u32x4_t sbv[SBCH];
@@ -115,28 +114,32 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
     const long off = min((long)n0 * G + 8 * cc, (long)N * G - 8);  // in bounds of expert e's block
     sbv[j] = ldg128(base + e * sstride + off);
   }
+  // ---- 4. x rows of pass 0 (waits only for the row indices, issued first)
+  u32x4_t xv[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (BITS == 4) swap_pairs(wsl);
 
-  f32x4_t acc;
+  const u16* xl = &xs[min(c16, RC - 1) * XP + k_quarter<BITS>(q)];
+  const int nrow = max(n - (ncol - c16), 0);  // this lane's row in its tile block (0 past N)
+  const u32* sp = reinterpret_cast<const u32*>(&sbl[0][tile][nrow * G + gs]);
+  const u32* bp = reinterpret_cast<const u32*>(&sbl[1][tile][nrow * G + gs]);
   for (int r0 = 0; r0 < m_rows; r0 += RC) {
     const int rows = min(RC, m_rows - r0);
     if (r0 > 0) {
 #pragma unroll
       for (int i = 0; i < XCH; ++i) src[i] = src_row(r0, xrow[i]);
+#pragma unroll
+      for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
       __syncthreads();  // the previous pass has finished with xs, xsum and red
     }
-    // ---- 3. x rows of the pass -> LDS with their per-group sums (8 lanes per (row, group))
-    u32x4_t xv[XCH];
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
+    // ---- 5. x rows -> LDS with their per-group sums (8 lanes per (row, group))
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
       const bool valid = tid + 256 * i < xtotal;
       u32x4_t v = xv[i];
-      float s8 = sum_bf16x8(v);
-      s8 += shfl_xor(s8, 1);
-      s8 += shfl_xor(s8, 2);
-      s8 += shfl_xor(s8, 4);
+      float s8 = sum8_lanes(sum_bf16x8(v));
       if (BITS == 4) {
         v = perm_x_u4(v);
         s8 *= -128.0f;
@@ -157,35 +160,37 @@ __global__ __launch_bounds__(256, (KSMAX >= 32 || BITS == 8) ? 2 : 3) void moe_r
       }
     }
     __syncthreads();
-    // ---- 4. MFMA over the wave's groups (A rows >= RC repeat row RC-1). The empty asm makes
-    // the weight registers opaque per pass, so the compiler cannot hoist the dequantized
-    // fragments of every group out of the pass loop (they would need 8 registers per group).
+    // ---- 6. MFMA over the wave's groups, two at a time (the part's group count is even and
+    // wave-uniform). A rows >= RC repeat row RC-1. The empty asm makes the weight registers
+    // opaque per pass, so the compiler cannot hoist every group's dequantized fragments out of
+    // the pass loop.
 #pragma unroll
     for (int j = 0; j < (BITS == 4 ? KSMAX / 2 : KSMAX); ++j) asm volatile("" : "+v"(wsl.v[j]));
-    acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const u16* xl = &xs[min(c16, RC - 1) * XP + k_quarter<BITS>(q)];
-    const int nrow = max(n - (ncol - c16), 0);  // this lane's row in its tile block (0 past N)
-    const u32* sp = reinterpret_cast<const u32*>(&sbl[0][tile][nrow * G + gs]);
-    const u32* bp = reinterpret_cast<const u32*>(&sbl[1][tile][nrow * G + gs]);
-    u32x2_t w4[2] = {};
-    u32 sp2 = 0, bp2 = 0;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int gl = 0; gl < KSMAX; ++gl) {
-      if (gl < gcount) {
-        if (BITS == 4 && (gl & 1) == 0) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
-        const int g = gs + gl;
+    for (int gl = 0; gl < KSMAX; gl += 2) {
+      if (gl >= gcount) break;  // wave-uniform
+      const int gp = gl;
+      const u32 s2 = sp[gp >> 1], b2 = bp[gp >> 1];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int g = gs + gp + h;
         const u32x4_t a0 = lds128(xl + 64 * g), a1 = lds128(xl + 64 * g + 8);
         const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[g][0]);
-        if ((gl & 1) == 0) {
-          sp2 = sp[gl >> 1];
-          bp2 = bp[gl >> 1];
+        u32x2_t w4 = {};
+        u32x4_t w8 = {};
+        if constexpr (BITS == 4) {
+          const u32x4_t& v = wsl.v[gl >> 1];
+          w4 = h ? u32x2_t{v.z, v.w} : u32x2_t{v.x, v.y};
+        } else {
+          w8 = wsl.v[gl + h];
         }
-        const u32 sb = (gl & 1) ? (sp2 >> 16) : (sp2 & 0xFFFFu);
-        const u32 bb = (gl & 1) ? (bp2 >> 16) : (bp2 & 0xFFFFu);
-        group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : gl], w4[gl & 1], bf2f(sb), bf2f(bb), acc);
+        const u32 sb = h ? (s2 >> 16) : (s2 & 0xFFFFu);
+        const u32 bb = h ? (b2 >> 16) : (b2 & 0xFFFFu);
+        group_fma<BITS>(a0, a1, c, w8, w4, bf2f(sb), bf2f(bb), acc);
       }
     }
-    // ---- 5. partial tiles (rows 0..RC-1 live in lanes q == 0) -> LDS, summed in part order
+    // ---- 7. partial tiles (rows 0..RC-1 live in lanes q == 0) -> LDS, summed in part order
     if (q == 0) {
 #pragma unroll
       for (int r = 0; r < RC; ++r) red[wave][r * 16 + c16] = acc[r];

@@ -10,7 +10,7 @@ namespace dspark {
 // bf16 pair (128 + nibble t, 128 + nibble t+4) of a packed 4-bit word, for t = 0..3.
 __device__ __forceinline__ u32x4_t unpack_u4(u32 w) {
   const u32 m = 0x000F000Fu, c = 0x43004300u;
-  return u32x4_t{(w & m) | c, ((w >> 4) & m) | c, ((w >> 8) & m) | c, ((w >> 12) & m) | c};
+  return u32x4_t{and_or(w, m, c), and_or(w >> 4, m, c), and_or(w >> 8, m, c), and_or(w >> 12, m, c)};
 }
 
 // Reorders 8 consecutive bf16 x-values [x0..x7] into [x0,x4,x1,x5,x2,x6,x3,x7], the field

@@ -110,6 +110,18 @@ struct WSlice {
   }
 };
 
+// In place: every 4-bit load j becomes {group 2j lo, hi, group 2j+1 lo, hi} of this lane
+// (the exchange frag_u4 performs).
+template <int KSMAX>
+__device__ __forceinline__ void swap_pairs(WSlice<4, KSMAX>& w) {
+#pragma unroll
+  for (int j = 0; j < KSMAX / 2; ++j) {
+    const auto r0 = __builtin_amdgcn_permlane32_swap(w.v[j].x, w.v[j].z, false, false);
+    const auto r1 = __builtin_amdgcn_permlane32_swap(w.v[j].y, w.v[j].w, false, false);
+    w.v[j] = u32x4_t{r0[0], r1[0], r0[1], r1[1]};
+  }
+}
+
 // (words of group 2j, words of group 2j+1) of 4-bit load j, each {k 16qs..+7, k 16qs+8..+15}
 __device__ __forceinline__ void frag_u4(u32x4_t v, u32x2_t& f0, u32x2_t& f1) {
   const auto r0 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
