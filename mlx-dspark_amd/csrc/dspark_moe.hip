@@ -16,6 +16,8 @@
 // (counting sort, stable in pair id). The grouped qmm launches one workgroup per
 // (expert, 16-feature tile); workgroups of unselected experts exit at once, every selected
 // expert's weight tile is streamed once for all of its tokens (<= 16 at verify widths).
+#include <initializer_list>
+
 #include "dspark_moe_rc.h"
 #include "dspark_moe_sk.h"
 
@@ -407,11 +409,10 @@ MoePlan moe_plan(long K, long N, long E, long M, bool swiglu, int bits) {
   long s = (G + 15) / 16;
   if (E * p.strips * p.mtiles * s < 512) s = (G + 7) / 8;
   if (s > kQmmMaxSlices) s = kQmmMaxSlices;
-  if (s < (G + 31) / 32) s = (G + 31) / 32;
   if (s < 1) s = 1;
   p.S = (int)s;
   p.ksmax = slice_capacity(G, s, bits);
-  p.sbvec = (G % s == 0) && ((G / s) % 8 == 0);
+  p.sbvec = G % 8 == 0;
   p.ctrs = (size_t)E * p.strips * p.mtiles;
   p.part_floats = p.S > 1 ? p.ctrs * p.S * 1024 : 0;
   return p;
@@ -440,6 +441,12 @@ MoeWorkspace moe_layout(long M, long H, long I, long E, long k, int bits) {
   w.part = o;    o += align256(sizeof(float) * (w.gu.part_floats > w.dn.part_floats ? w.gu.part_floats : w.dn.part_floats));
   w.total = o;
   return w;
+}
+
+// The plan with 16-byte scale/bias loads only if every scale/bias array is 16-byte aligned.
+MoePlan sb_checked(MoePlan p, std::initializer_list<const void*> arrays) {
+  for (const void* a : arrays) p.sbvec = p.sbvec && aligned(a, 16);
+  return p;
 }
 
 MoeRcArgs rc_args(const MoeSkArgs& a) {
@@ -520,8 +527,7 @@ int launch_moe_sk(const MoeSkArgs& a, const MoePlan& p, int E, int bits, hipStre
 #define MOE_SK(B, KS, SB) hipLaunchKernelGGL((moe_sk_kernel<B, KS, SB, SWIGLU>), grid, dim3(256), 0, s, a)
 #define MOE_SK_BITS(B)                                                   \
   if (p.ksmax == 8) { if (p.sbvec) MOE_SK(B, 8, true); else MOE_SK(B, 8, false); }     \
-  else if (p.ksmax == 16) { if (p.sbvec) MOE_SK(B, 16, true); else MOE_SK(B, 16, false); } \
-  else { if (p.sbvec) MOE_SK(B, 32, true); else MOE_SK(B, 32, false); }
+  else { if (p.sbvec) MOE_SK(B, 16, true); else MOE_SK(B, 16, false); }
   if (bits == 4) { MOE_SK_BITS(4) } else { MOE_SK_BITS(8) }
 #undef MOE_SK_BITS
 #undef MOE_SK
@@ -662,7 +668,7 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   const RcPlan rgu = rc_plan(H, I, true, s_gate, b_gate), rgu2 = rc_plan(H, I, true, s_up, b_up);
   if (rgu.kw && rgu2.kw) {
     if ((st = launch_moe_rc<true>(rc_args(g), rgu, (int)E, bits, s))) return st;
-  } else if ((st = launch_moe_sk<true>(g, L.gu, (int)E, bits, s))) {
+  } else if ((st = launch_moe_sk<true>(g, sb_checked(L.gu, {s_gate, b_gate, s_up, b_up}), (int)E, bits, s))) {
     return st;
   }
 
@@ -688,7 +694,7 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   const RcPlan rdn = rc_plan(I, H, false, s_down, b_down);
   if (rdn.kw) {
     if ((st = launch_moe_rc<false>(rc_args(d), rdn, (int)E, bits, s))) return st;
-  } else if ((st = launch_moe_sk<false>(d, L.dn, (int)E, bits, s))) {
+  } else if ((st = launch_moe_sk<false>(d, sb_checked(L.dn, {s_down, b_down}), (int)E, bits, s))) {
     return st;
   }
 

@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_r
   // K parts start on even groups (G is even): weights of 4-bit rows and the scale/bias
   // pairs are read two groups at a time
   int gs, ge;
-  slice_groups<4>(kp, KW, G, gs, ge);
+  slice_groups(kp, KW, G, 2, gs, ge);
   const int gcount = ge - gs;  // even, >= 2
   const bool up = SWIGLU && (tile & 1);
   const int ncol = SWIGLU ? strip * (8 * NT) + 16 * (tile >> 1) + c16 : strip * (16 * NT) + 16 * tile + c16;

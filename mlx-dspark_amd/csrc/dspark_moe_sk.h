@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void moe_sk_kernel(const MoeSkArgs a) {
   const int S = a.S, K = a.K, N = a.N;
   const int G = K >> 6;
   int gs, ge;
-  slice_groups<BITS>(sl, S, G, gs, ge);
+  slice_groups(sl, S, G, slice_unit(G, BITS), gs, ge);
   const int gcount = ge - gs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q = lane >> 4;
@@ -162,20 +162,21 @@ __global__ __launch_bounds__(256) void moe_sk_kernel(const MoeSkArgs a) {
       last_flag = (__hip_atomic_fetch_add(&a.ctr[tix], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1);
     __syncthreads();
     if (!last_flag) return;
-    float pv[4][kQmmMaxSlices];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r) v[r] = 0.f;
+    for (int s0 = 0; s0 < S; s0 += kSliceChunk) {  // slice order, kSliceChunk requests at a time
+      float pv[4][kSliceChunk];
 #pragma unroll
-      for (int s2 = 0; s2 < kQmmMaxSlices; ++s2)
-        pv[r][s2] = __hip_atomic_load(&part[(long)min(s2, S - 1) * 1024 + (4 * q + r) * 64 + tcol],
-                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float t = 0.f;
+        for (int s2 = 0; s2 < kSliceChunk; ++s2)
+          pv[r][s2] = __hip_atomic_load(&part[(long)min(s0 + s2, S - 1) * 1024 + (4 * q + r) * 64 + tcol],
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-      for (int s2 = 0; s2 < kQmmMaxSlices; ++s2)
-        if (s2 < S) t += pv[r][s2];
-      v[r] = t;
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int s2 = 0; s2 < kSliceChunk; ++s2)
+          if (s0 + s2 < S) v[r] += pv[r][s2];
     }
     if (tid == 0) __hip_atomic_store(&a.ctr[tix], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }

@@ -62,10 +62,13 @@ Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
   long s = (G + 15) / 16;
   if (strips * s < kTargetWorkgroups) s = (G + 7) / 8;
   if (s > kQmmMaxSlices) s = kQmmMaxSlices;
-  if (s < (G + 31) / 32) s = (G + 31) / 32;  // a slice holds at most 32 groups
   if (s < 1) s = 1;
   p.S = (int)s;
   p.ksmax = slice_capacity(G, s, bits);
+  if (!p.ksmax) {
+    p.S = 0;  // refused: K too large for 32 slices of 16 groups
+    return p;
+  }
   if (p.S > 1) {
     const size_t ctrs = (size_t)strips * p.mtiles;
     if (ctrs > kMaxCounters) {
@@ -87,8 +90,7 @@ int launch(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
 template <int BITS>
 int launch_bits(const QmmSkArgs& a, const Plan& p, bool sbvec, hipStream_t st) {
   if (p.ksmax == 8) return sbvec ? launch<BITS, 8, true>(a, p, st) : launch<BITS, 8, false>(a, p, st);
-  if (p.ksmax == 16) return sbvec ? launch<BITS, 16, true>(a, p, st) : launch<BITS, 16, false>(a, p, st);
-  return sbvec ? launch<BITS, 32, true>(a, p, st) : launch<BITS, 32, false>(a, p, st);
+  return sbvec ? launch<BITS, 16, true>(a, p, st) : launch<BITS, 16, false>(a, p, st);
 }
 
 int check_common(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
@@ -138,8 +140,8 @@ extern "C" int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int 
   if (st) return st;
   long Ns[1] = {(long)N};
   if (make_plan(Ns, 1, K, M, bits).S == 0)
-    return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld x N=%lld needs more than %zu split-K counters", (long long)M,
-                (long long)N, kMaxCounters);
+    return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld x N=%lld x K=%lld needs more than %zu split-K counters or 32 slices",
+                (long long)M, (long long)N, (long long)K, kMaxCounters);
   return DSPARK_OK;
 }
 
@@ -180,13 +182,14 @@ extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int c
   const long K = problems[0].K;
   const Plan p = make_plan(Ns, count, K, M, bits);
   if (p.S == 0)
-    return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld needs more than %zu split-K counters", (long long)M, kMaxCounters);
+    return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld K=%lld needs more than %zu split-K counters or 32 slices", (long long)M,
+                (long long)K, kMaxCounters);
   const size_t need = p.ctr_bytes + p.part_bytes;
   if (need && (!workspace || workspace_bytes < need))
     return fail(DSPARK_ERR_WORKSPACE, "qmm: workspace %zu < %zu bytes", workspace_bytes, need);
   if (need && !aligned(workspace, 256)) return fail(DSPARK_ERR_ALIGN, "qmm: workspace must be 256-byte aligned");
   const long G = K / 64;
-  bool sbvec = (G % p.S == 0) && ((G / p.S) % 8 == 0);
+  bool sbvec = G % 8 == 0;
   QmmSkArgs a{};
   a.count = count;
   a.M = (int)M;

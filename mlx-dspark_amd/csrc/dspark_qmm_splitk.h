@@ -19,7 +19,8 @@
 namespace dspark {
 
 constexpr int kQmmMaxProblems = DSPARK_QMM_MAX_PROBLEMS;
-constexpr int kQmmMaxSlices = 16;
+constexpr int kQmmMaxSlices = 32;
+constexpr int kSliceChunk = 8;  // partials the last arriver requests at a time
 
 struct QmmSkProb {
   const u16* x;
@@ -59,25 +60,24 @@ __device__ __forceinline__ float sum_bf16x8(u32x4_t v) {
   return s;
 }
 
-// Groups [gs, ge) of K slice sl of S (G groups per row). 4-bit slices start on an even group
-// because their weights are read two groups per load (see WSlice).
-template <int BITS>
-__device__ __forceinline__ void slice_groups(int sl, int S, int G, int& gs, int& ge) {
-  if constexpr (BITS == 4) {
-    const int pairs = (G + 1) >> 1;
-    gs = 2 * ((sl * pairs) / S);
-    ge = min(2 * (((sl + 1) * pairs) / S), G);
-  } else {
-    gs = (sl * G) / S;
-    ge = ((sl + 1) * G) / S;
-  }
+// K slices are cut on multiples of `unit` groups: 8 when G is a multiple of 8 (every slice's
+// scale/bias run is then whole 16-byte chunks), else 2 for 4-bit rows (their weights are read
+// two groups per load, see WSlice), else 1.
+__host__ __device__ inline int slice_unit(int G, int bits) { return G % 8 == 0 ? 8 : bits == 4 ? 2 : 1; }
+
+// Groups [gs, ge) of K slice sl of S (S <= ceil(G / unit), so no slice is empty).
+__host__ __device__ inline void slice_groups(int sl, int S, int G, int unit, int& gs, int& ge) {
+  const int units = (G + unit - 1) / unit;
+  gs = unit * ((sl * units) / S);
+  ge = min(unit * (((sl + 1) * units) / S), G);
 }
 
-// Kernel instantiation (8, 16 or 32 groups) that holds the largest of S slices of G groups,
-// as slice_groups() cuts them.
+// Kernel instantiation (8 or 16 groups) that holds the largest of S slices of G groups, or 0
+// when a slice would exceed 16 groups (K > 32768 at 32 slices).
 inline int slice_capacity(long G, long S, int bits) {
-  const long per = bits == 4 ? 2 * (((G + 1) / 2 + S - 1) / S) : (G + S - 1) / S;
-  return per <= 8 ? 8 : per <= 16 ? 16 : 32;
+  const long unit = slice_unit((int)G, bits), units = (G + unit - 1) / unit;
+  const long per = unit * ((units + S - 1) / S);
+  return per <= 8 ? 8 : per <= 16 ? 16 : 0;
 }
 
 // The weight fragments of one row over a K slice, loaded with 16-byte loads.
@@ -163,6 +163,10 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   // per group: 16 row sums (8-bit: sum x; 4-bit: -128 * sum x, the MFMA seed)
   __shared__ __attribute__((aligned(16))) float xsum[KSMAX * 16];
   __shared__ int last_flag;
+  // SBVEC: scales (0) and biases (1) of the strip's 16*NS rows over the slice, row pitch
+  // SBP (16-byte rows; 4-byte reads of 16 consecutive rows fall in distinct banks)
+  constexpr int SBP = KSMAX + 8;
+  __shared__ __attribute__((aligned(16))) u16 sbl[SBVEC ? 2 : 1][SBVEC ? 16 * NS : 1][SBVEC ? SBP : 1];
 
   const int bx = blockIdx.x;
   int pi = 0;
@@ -177,13 +181,13 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   const int mt = blockIdx.z;
   const int G = K >> 6;
   int gs, ge;
-  slice_groups<BITS>(sl, S, G, gs, ge);
+  slice_groups(sl, S, G, slice_unit(G, BITS), gs, ge);
   const int gcount = ge - gs;
   const int m_base = mt * 16;
   const int m_rows = min(16, args.M - m_base);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = uniform(tid >> 6);
   const int c16 = lane & 15, q = lane >> 4;
   const int ncol = strip * 16 * NS + 16 * wave + c16;
   const int n = min(ncol, N - 1);
@@ -210,21 +214,24 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   // ---- 2. every weight load of this lane's row in the slice (clamped, unconditional)
   WSlice<BITS, KSMAX> wsl;
   wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
-  // ---- 3. scales / biases of the row's groups in the slice
-  constexpr int SBV = (KSMAX + 7) / 8;
-  u32x4_t svv[SBV], bvv[SBV];
+  // ---- 3. scales / biases of the strip's rows over the slice. SBVEC (G a multiple of 8, so
+  // slices are too; 16-byte aligned arrays): the workgroup reads them as 16-byte chunks,
+  // one (array, row, 8 groups) each, into LDS. Otherwise every lane reads its own row's.
+  constexpr int SBCH = SBVEC ? (2 * 16 * NS * (KSMAX / 8) + 64 * NS - 1) / (64 * NS) : 1;
+  u32x4_t sbv[SBCH];
   u32 svs[SBVEC ? 1 : KSMAX], bvs[SBVEC ? 1 : KSMAX];
-  const u16* srow = P.s + (long)n * G + gs;
-  const u16* brow = P.b + (long)n * G + gs;
+  const int cpa = 16 * NS * (gcount >> 3);  // chunks per array
   if constexpr (SBVEC) {
-    // gcount is a multiple of 8 and the row/slice starts are 16-byte aligned
 #pragma unroll
-    for (int j = 0; j < SBV; ++j) {
-      const int jj = min(j, (gcount >> 3) - 1);
-      svv[j] = ldg128(srow + 8 * jj);
-      bvv[j] = ldg128(brow + 8 * jj);
+    for (int j = 0; j < SBCH; ++j) {
+      const int ci = min(tid + 64 * NS * j, 2 * cpa - 1);
+      const int arr = ci / cpa, r = (ci % cpa) / (gcount >> 3), jj = ci % (gcount >> 3);
+      const int nr = min(strip * 16 * NS + r, N - 1);
+      sbv[j] = ldg128((arr ? P.b : P.s) + (long)nr * G + gs + 8 * jj);
     }
   } else {
+    const u16* srow = P.s + (long)n * G + gs;
+    const u16* brow = P.b + (long)n * G + gs;
 #pragma unroll
     for (int gl = 0; gl < KSMAX; ++gl) {
       const int g = min(gl, gcount - 1);
@@ -245,10 +252,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     const int c = min(c0, xtotal - 1);
     const int row = c / cpr, col = c - row * cpr;
     u32x4_t v = xv[i];
-    float s8 = sum_bf16x8(v);
-    s8 += shfl_xor(s8, 1);
-    s8 += shfl_xor(s8, 2);
-    s8 += shfl_xor(s8, 4);
+    float s8 = sum8_lanes(sum_bf16x8(v));
     if (BITS == 4) {
       // store the 8 values in the (t, t+4) order unpack_u4 produces
       v = perm_x_u4(v);
@@ -257,29 +261,49 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     *reinterpret_cast<u32x4_t*>(&xs[row * XP + (valid ? 8 * col : KSMAX * 64)]) = v;
     if (valid && (c & 7) == 0) xsum[(col >> 3) * 16 + row] = s8;
   }
+  if constexpr (SBVEC) {
+#pragma unroll
+    for (int j = 0; j < SBCH; ++j) {
+      const int ci = tid + 64 * NS * j;
+      if (ci < 2 * cpa) {
+        const int arr = ci / cpa, r = (ci % cpa) / (gcount >> 3), jj = ci % (gcount >> 3);
+        *reinterpret_cast<u32x4_t*>(&sbl[arr][r][8 * jj]) = sbv[j];
+      }
+    }
+  }
   __syncthreads();
 
-  // ---- 5. MFMA loop over the slice
+  // ---- 5. MFMA loop over the slice, a pair of groups per step (gcount is wave-uniform)
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   const u16* xl = &xs[c16 * XP + k_quarter<BITS>(q)];
-  u32x2_t w4[2] = {};
+  const int srow_l = SBVEC ? 16 * wave + c16 : 0;
 #pragma unroll
-  for (int gl = 0; gl < KSMAX; ++gl) {
-    if (gl < gcount) {
-      if (BITS == 4 && (gl & 1) == 0) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
-      const u32x4_t a0 = lds128(xl + 64 * gl), a1 = lds128(xl + 64 * gl + 8);
+  for (int gl = 0; gl < KSMAX; gl += 2) {
+    if (gl >= gcount) break;
+    u32x2_t w4[2] = {};
+    if constexpr (BITS == 4) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
+    u32 s2 = 0, b2 = 0;
+    if constexpr (SBVEC) {
+      s2 = *reinterpret_cast<const u32*>(&sbl[0][srow_l][gl]);
+      b2 = *reinterpret_cast<const u32*>(&sbl[1][srow_l][gl]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && gl + 1 >= gcount) break;
+      const int g = gl + h;
+      const u32x4_t a0 = lds128(xl + 64 * g), a1 = lds128(xl + 64 * g + 8);
       // rows 4q..4q+3. (Read as a float vector: bit-casting ext-vector elements one by one
       // miscompiles to a single-dword read.)
-      const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[gl * 16 + 4 * q]);
+      const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&xsum[g * 16 + 4 * q]);
       u32 sbits, bbits;
       if constexpr (SBVEC) {
-        sbits = bf_field(svv[gl >> 3], gl & 7);
-        bbits = bf_field(bvv[gl >> 3], gl & 7);
+        sbits = h ? (s2 >> 16) : (s2 & 0xFFFFu);
+        bbits = h ? (b2 >> 16) : (b2 & 0xFFFFu);
       } else {
-        sbits = svs[gl];
-        bbits = bvs[gl];
+        sbits = svs[g];
+        bbits = bvs[g];
       }
-      group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : gl], w4[gl & 1], bf2f(sbits), bf2f(bbits), acc);
+      group_fma<BITS>(a0, a1, c, wsl.v[BITS == 4 ? 0 : g], w4[h], bf2f(sbits), bf2f(bbits), acc);
     }
   }
 
@@ -310,25 +334,31 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   __syncthreads();
   if (!last_flag) return;
   // 16*TW outputs, 4 per thread; all S partials of all 4 are requested before summing
-  float pv[4][kQmmMaxSlices];
+  // 16*TW outputs, 4 per thread, summed in slice order; kSliceChunk slices are requested
+  // at a time for all 4
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += kSliceChunk) {
+    float pv[4][kSliceChunk];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid + i * 64 * NS;
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + i * 64 * NS;
 #pragma unroll
-    for (int s2 = 0; s2 < kQmmMaxSlices; ++s2)
-      pv[i][s2] = __hip_atomic_load(&part[(long)min(s2, S - 1) * (16 * TW) + e], __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+      for (int s2 = 0; s2 < kSliceChunk; ++s2)
+        pv[i][s2] = __hip_atomic_load(&part[(long)min(s0 + s2, S - 1) * (16 * TW) + e], __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int s2 = 0; s2 < kSliceChunk; ++s2)
+        if (s0 + s2 < S) v[i] += pv[i][s2];
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = tid + i * 64 * NS;
     const int m = e / TW, col = e - m * TW;
-    float v = 0.f;
-#pragma unroll
-    for (int s2 = 0; s2 < kQmmMaxSlices; ++s2)
-      if (s2 < S) v += pv[i][s2];
     const int nc = strip * TW + col;
-    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v);
+    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v[i]);
   }
   if (tid == 0) __hip_atomic_store(&P.ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -25,7 +25,7 @@ from . import _lib, ops
 GROUP = 64
 RT_MAX = 1                              # 16-row tiles per workgroup (one MFMA row tile)
 WINDOW = {4: (1, 16), 8: (1, 16)}       # rows served per quantization width
-S_MAX = 16                              # most K slices a launch splits into
+S_MAX = 32                              # most K slices a launch splits into
 _s_cap = S_MAX
 
 
