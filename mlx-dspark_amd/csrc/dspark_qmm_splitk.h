@@ -4,11 +4,10 @@
 // K (blockIdx.y). The slice of x (16 rows x slice) is staged once in LDS and shared by the NS
 // waves, together with its per-group row sums (the bias term's sum_j x[m, j], reduced across
 // 8 lanes during staging). Load order is what keeps this a single memory round trip: every
-// x-slice load of the thread is issued first, then every weight load of its 16 rows x slice
-// (one 16/8-byte load per row-group per lane, straight from the packed row), then the scales
-// and biases (8 groups per 16-byte load). Vector-memory completion is counted in issue order,
-// so waiting for x does not wait for the weight stream; the MFMA loop then consumes weights
-// as they land, reading x fragments from LDS.
+// x-slice load of the thread is issued first, then the strip's scales and biases, then every
+// weight load of its 16 rows x slice (16-byte loads straight from the packed rows).
+// Vector-memory completion is counted in issue order, so staging x, scales and biases in LDS
+// does not wait for the weight stream; the MFMA loop then consumes weights as they land.
 // Slices of one strip are combined by the last workgroup to finish (a device-scope arrival
 // counter per strip), always in slice order 0..S-1, so the result is deterministic and
 // independent of M and of arrival order.
@@ -211,10 +210,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
       xv[i] = ldg128(xb + (long)src * P.ldx + 8 * col);
     }
   }
-  // ---- 2. every weight load of this lane's row in the slice (clamped, unconditional)
-  WSlice<BITS, KSMAX> wsl;
-  wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
-  // ---- 3. scales / biases of the strip's rows over the slice. SBVEC (G a multiple of 8, so
+  // ---- 2. scales / biases of the strip's rows over the slice. SBVEC (G a multiple of 8, so
   // slices are too; 16-byte aligned arrays): the workgroup reads them as 16-byte chunks,
   // one (array, row, 8 groups) each, into LDS. Otherwise every lane reads its own row's.
   constexpr int SBCH = SBVEC ? (2 * 16 * NS * (KSMAX / 8) + 64 * NS - 1) / (64 * NS) : 1;
@@ -239,10 +235,13 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
       bvs[gl] = brow[g];
     }
   }
+  // ---- 3. every weight load of this lane's row in the slice (clamped, unconditional)
+  WSlice<BITS, KSMAX> wsl;
+  wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
   // every load above is issued before anything consumes one (keeps the scheduler from
   // interleaving the x processing, and its waits, into the load sequence)
   __builtin_amdgcn_sched_barrier(0);
-  // ---- 4. x slice -> LDS with the group sums (8-lane xor-shuffle reduction). Branch-free, so
+  // ---- 4. x slice -> LDS with the group sums (8-lane butterfly reduction). Branch-free, so
   // the compiler cannot sink a load into a conditional block behind the weight stream: a chunk
   // past the slice (whole waves only) lands in the row's unused 16-byte pad.
 #pragma unroll
