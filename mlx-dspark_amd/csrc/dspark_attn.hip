@@ -9,9 +9,9 @@
 // (multirow_attn.py:162-178).
 //
 // MI355X mapping:
-//   * grid = (B*Hk, NB key blocks, row groups); a 256-thread workgroup (4 waves) owns one KV
-//     head's key block and up to 4 row tiles of 16 rows (all gqa*Mq rows of the head when
-//     they fit), so each K/V byte is read from HBM once per workgroup and shared by every
+//   * grid = (B*Hk, NB key blocks, row groups); a workgroup of 4 or 8 waves owns one KV
+//     head's key block and up to 4 or 8 row tiles of 16 rows (all gqa*Mq rows of the head
+//     when there are at most 128), so each K/V byte is read from HBM once and shared by every
 //     query head of the GQA group.
 //   * 64-key tiles are staged through LDS with register double buffering: K row-major
 //     (padded rows), V transposed (key-contiguous, 8-key blocks XOR-swizzled by d) because the
@@ -26,8 +26,6 @@ namespace dspark {
 namespace {
 
 constexpr int KT = 64;      // keys per LDS tile
-constexpr int WAVES = 4;    // row tiles per workgroup
-constexpr int THREADS = 64 * WAVES;
 
 struct AttnArgs {
   const u16* q;
@@ -54,13 +52,19 @@ __device__ __forceinline__ int vt_pos(int key) {
   const int u = key >> 5, h = (key >> 4) & 1, qq = (key >> 2) & 3, i = key & 3;
   return (u << 5) | (qq << 3) | (h << 2) | i;
 }
+// 2^x with v_exp_f32 (results below 2^-126 flush to 0: negligible softmax weights)
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // swizzled element offset of (d, pos) in the transposed V tile (row pitch KT)
 __device__ __forceinline__ int vt_off(int d, int pos) {
   return d * KT + ((((pos >> 3) ^ (d >> 1) ^ (d >> 3)) & 7) << 3) + (pos & 7);
 }
 
-template <int D, bool TREE>
-__global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
+// WV waves = WV row tiles per workgroup (4, or 8 when a KV head has more than 4 row tiles, so
+// every row of the head shares one read of each K/V tile).
+template <int D, bool TREE, int WV>
+__global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
+  constexpr int THREADS = 64 * WV;
   constexpr int KP = D + 8;           // padded K row (elements)
   constexpr int DC = D / 8;           // 16-byte chunks per key row
   constexpr int LOADS = KT * DC / THREADS;  // 16-byte K chunks per thread per tile
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int rt = blockIdx.z * WAVES + wave;
+  const int rt = blockIdx.z * WV + wave;
   const bool active = rt < a.RT;
 
   const int L = a.L;
@@ -168,39 +172,49 @@ __global__ __launch_bounds__(THREADS) void attn_p1_kernel(const AttnArgs a) {
         s[ks] = mfma16x16x32(kf, qf[c], s[ks]);
       }
     }
-    // mask + scale, row max
-    float mloc = -INFINITY;
+    // row max of the raw scores (invisible keys -inf; only a chunk's last tile, the causal
+    // diagonal and the tree block need the mask). The scale is applied in the exponent:
+    // p = 2^(s * scale - m) with m the running max of the scaled scores.
+    const bool edge = (kt + KT > k1) || (TREE ? (kt + KT > tail0) : (a.causal && kt + KT - 1 > L - a.Mq));
+    float smax = -INFINITY;
+    if (edge) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kt + 16 * ks + 4 * q4 + i;
-        bool vis = key < k1;
-        if (TREE)
-          vis = vis && (key < tail0 || ((anc >> ((unsigned)(key - tail0) & 31u)) & 1u));
-        else
-          vis = vis && key <= kmax;
-        const float sv = vis ? s[ks][i] * a.scale_log2 : -INFINITY;
-        s[ks][i] = sv;
-        mloc = fmaxf(mloc, sv);
-      }
-    mloc = fmaxf(mloc, shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-    const float mn = fmaxf(m, mloc);
-    const float alpha = exp2f(m - mn);
+        for (int i = 0; i < 4; ++i) {
+          const int key = kt + 16 * ks + 4 * q4 + i;
+          bool vis = key < k1;
+          if (TREE)
+            vis = vis && (key < tail0 || ((anc >> ((unsigned)(key - tail0) & 31u)) & 1u));
+          else
+            vis = vis && key <= kmax;
+          s[ks][i] = vis ? s[ks][i] : -INFINITY;
+          smax = fmaxf(smax, s[ks][i]);
+        }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) smax = fmaxf(smax, s[ks][i]);
+    }
+    smax = fmaxf(smax, shfl_xor(smax, 16));
+    smax = fmaxf(smax, shfl_xor(smax, 32));
+    const float mn = fmaxf(m, smax * a.scale_log2);
+    const float alpha = exp2_raw(m - mn);
     m = mn;
     float ps = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = exp2f(s[ks][i] - mn);
+        const float p = exp2_raw(__builtin_fmaf(s[ks][i], a.scale_log2, -mn));
         s[ks][i] = p;
         ps += p;
       }
     l = l * alpha + ps;
     // P as a bf16 pair hi + lo (hi = bf16(p), lo = bf16(p - hi)): the P.V product keeps ~16
-    // significant bits of p, so the bf16 output rounding is the only error of note.
+    // significant bits of p, so the bf16 output rounding is the only error of note (a single
+    // bf16 P, as the reference's kernel rounds it, leaves little margin on long flat rows).
     u32x4_t ph[2], pl[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -325,7 +339,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
 }
 
 struct Plan {
-  int R, RT, RP, NRG, chunk, NB;
+  int R, RT, RP, WV, NRG, chunk, NB;
 };
 
 Plan make_plan(long B, long Hq, long Hk, long Mq, long L) {
@@ -333,9 +347,11 @@ Plan make_plan(long B, long Hq, long Hk, long Mq, long L) {
   p.R = (int)((Hq / Hk) * Mq);
   p.RT = (p.R + 15) / 16;
   p.RP = p.RT * 16;
-  p.NRG = (p.RT + WAVES - 1) / WAVES;
+  p.WV = p.RT > 4 ? 8 : 4;
+  p.NRG = (p.RT + p.WV - 1) / p.WV;
   // ~2 workgroups per CU (256 CUs) on long caches; at least 4 tiles (256 keys) per block so
-  // the fp32 partials stay a small fraction of the KV stream.
+  // the fp32 partials stay a small fraction of the KV stream. Row groups beyond one re-read
+  // the head's K/V (only when gqa * Mq > 128).
   const long heads = B * Hk * p.NRG;
   const long target = 512;
   long nb = (target + heads - 1) / heads;
@@ -458,13 +474,16 @@ int verify_attention_impl(const void* q, int64_t B, int64_t Hq, int64_t Mq, int6
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid1((unsigned)(B * Hk), (unsigned)p.NB, (unsigned)p.NRG);
   const bool tree = tree_anc != nullptr;
+#define ATTN_P1(DD, TR, W) hipLaunchKernelGGL((attn_p1_kernel<DD, TR, W>), grid1, dim3(64 * W), 0, s, a)
+#define ATTN_P1_W(DD, TR) \
+  if (p.WV == 8) ATTN_P1(DD, TR, 8); else ATTN_P1(DD, TR, 4);
   if (D == 128) {
-    if (tree) hipLaunchKernelGGL((attn_p1_kernel<128, true>), grid1, dim3(THREADS), 0, s, a);
-    else hipLaunchKernelGGL((attn_p1_kernel<128, false>), grid1, dim3(THREADS), 0, s, a);
+    if (tree) { ATTN_P1_W(128, true) } else { ATTN_P1_W(128, false) }
   } else {
-    if (tree) hipLaunchKernelGGL((attn_p1_kernel<64, true>), grid1, dim3(THREADS), 0, s, a);
-    else hipLaunchKernelGGL((attn_p1_kernel<64, false>), grid1, dim3(THREADS), 0, s, a);
+    if (tree) { ATTN_P1_W(64, true) } else { ATTN_P1_W(64, false) }
   }
+#undef ATTN_P1_W
+#undef ATTN_P1
   st = check_launch("verify_attention(p1)");
   if (st || p.NB == 1) return st;
   const dim3 grid2((unsigned)(B * Hk * p.R));
