@@ -114,6 +114,41 @@ int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int count, int64
 size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* problems, int count, int64_t M,
                                          int bits, int group_size);
 
+/*
+ * MI355X packed form of one quantized matrix. This build's own format, with no counterpart in
+ * the reference (whose checkpoints keep the layout above); callers that hold a matrix for many
+ * calls (a loaded model) pack it once. Weights go in 16-row tiles in the lane order of the MFMA
+ * loop, one 1 KB read per wave per group (8-bit) or group pair (4-bit), and scales/biases in
+ * 16-row x 8-group tiles. Every product of dspark_qmm_packed_multi equals that of
+ * dspark_qmm_affine_multi on the reference layout bit for bit.
+ * Requires K % 512 == 0 (K <= 32768), bits 4 or 8, group_size 64; any N (rows are padded to
+ * 16 with zeros).
+ */
+/* Bytes of the packed form (0 = shape not supported). */
+size_t dspark_qmm_packed_bytes(int64_t N, int64_t K, int bits, int group_size);
+
+/* Writes the packed form of (w, scales, biases) — the reference layout of dspark_qmm_affine,
+ * all 16-byte aligned — into `packed` (16-byte aligned, >= dspark_qmm_packed_bytes). */
+int dspark_qmm_pack(const uint32_t* w, const void* scales, const void* biases, int64_t N, int64_t K, int bits,
+                    int group_size, void* packed, size_t packed_bytes, dspark_stream stream);
+
+typedef struct dspark_qmm_packed_problem {
+  const void* x;
+  int64_t ldx;
+  const void* packed;  /* dspark_qmm_pack output for [N, K] */
+  void* y;
+  int64_t ldy;
+  int64_t N;
+  int64_t K;
+} dspark_qmm_packed_problem;
+
+/* dspark_qmm_affine_multi over packed matrices (same x / y / M / workspace rules). */
+int dspark_qmm_packed_multi(const dspark_qmm_packed_problem* problems, int count, int64_t M, int bits,
+                            int group_size, void* workspace, size_t workspace_bytes, dspark_stream stream);
+
+size_t dspark_qmm_packed_multi_workspace(const dspark_qmm_packed_problem* problems, int count, int64_t M,
+                                         int bits, int group_size);
+
 /* ------------------------------------------------------------------ verify attention */
 
 /*

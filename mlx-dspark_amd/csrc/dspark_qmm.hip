@@ -81,16 +81,80 @@ Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
   return p;
 }
 
-template <int BITS, int KSMAX, bool SBVEC>
+template <int BITS, int KSMAX, bool SBVEC, bool PACKED = false>
 int launch(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
-  hipLaunchKernelGGL((qmm_sk_kernel<BITS, kNS, KSMAX, SBVEC>), dim3(p.strips, p.S, p.mtiles), dim3(64 * kNS), 0, st, a);
-  return check_launch("dspark_qmm_affine");
+  hipLaunchKernelGGL((qmm_sk_kernel<BITS, kNS, KSMAX, SBVEC, PACKED>), dim3(p.strips, p.S, p.mtiles), dim3(64 * kNS), 0,
+                     st, a);
+  return check_launch(PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
 }
 
 template <int BITS>
 int launch_bits(const QmmSkArgs& a, const Plan& p, bool sbvec, hipStream_t st) {
   if (p.ksmax == 8) return sbvec ? launch<BITS, 8, true>(a, p, st) : launch<BITS, 8, false>(a, p, st);
   return sbvec ? launch<BITS, 16, true>(a, p, st) : launch<BITS, 16, false>(a, p, st);
+}
+
+template <int BITS>
+int launch_packed(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
+  if (p.ksmax == 8) return launch<BITS, 8, true, true>(a, p, st);
+  return launch<BITS, 16, true, true>(a, p, st);
+}
+
+// ---- the packed form (dspark_qmm_pack). Per matrix, T = ceil(N/16) row tiles, G = K/64:
+//   tile stream  T x (8-bit: G groups | 4-bit: G/2 group pairs) x 64 lanes x 16 B: lane l of
+//                tile t holds row 16t + (l & 15), quarter q = l >> 4:
+//                  8-bit: bytes [16q, 16q+16) of the group;
+//                  4-bit: bytes [8qs, 8qs+8) of group 2j then of group 2j+1, qs = 2(q&1) + (q>>1)
+//                  (the lane order the MFMA loop uses; see WSlice);
+//   scale/bias   T x G/8 octets x {scales, biases} x 16 rows x 8 bf16.
+// Rows >= N are zero.
+struct PackedLayout {
+  long tiles, wchunks, schunks;
+  size_t bytes() const { return (size_t)(wchunks + schunks) * 16; }
+};
+PackedLayout packed_layout(long N, long K, int bits) {
+  PackedLayout L{};
+  const long G = K / 64;
+  L.tiles = (N + 15) / 16;
+  L.wchunks = L.tiles * (bits == 4 ? G / 2 : G) * 64;
+  L.schunks = L.tiles * (G / 8) * 32;
+  return L;
+}
+
+__global__ __launch_bounds__(256) void pack_kernel(const unsigned char* __restrict__ w, const u16* __restrict__ s,
+                                                   const u16* __restrict__ b, long N, int K, int bits, long wchunks,
+                                                   long schunks, unsigned char* __restrict__ out) {
+  const long c = (long)blockIdx.x * 256 + threadIdx.x;
+  const int G = K >> 6;
+  u32x4_t v = {0u, 0u, 0u, 0u};
+  if (c < wchunks) {
+    const int per_tile = bits == 4 ? (G >> 1) : G;
+    const long t = c / (per_tile * 64);
+    const int rem = (int)(c - t * per_tile * 64), j = rem >> 6, l = rem & 63;
+    const long r = 16 * t + (l & 15);
+    const int q = l >> 4;
+    if (r < N) {
+      if (bits == 8) {
+        v = ldg128(w + r * K + j * 64 + 16 * q);
+      } else {
+        const int qs = 2 * (q & 1) + (q >> 1);
+        const unsigned char* row = w + r * (K / 2);
+        const u32x2_t lo = ldg64(row + (2 * j) * 32 + 8 * qs), hi = ldg64(row + (2 * j + 1) * 32 + 8 * qs);
+        v = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+      }
+    }
+  } else if (c < wchunks + schunks) {
+    const long c2 = c - wchunks;
+    const long blk = c2 >> 5;
+    const int rem = (int)(c2 & 31), arr = rem >> 4, r16 = rem & 15;
+    const long t = blk / (G >> 3);
+    const int o = (int)(blk - t * (G >> 3));
+    const long r = 16 * t + r16;
+    if (r < N) v = ldg128((arr ? b : s) + r * G + 8 * o);
+  } else {
+    return;
+  }
+  *reinterpret_cast<u32x4_t*>(out + c * 16) = v;
 }
 
 int check_common(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
@@ -117,12 +181,15 @@ int check_problem(const dspark_qmm_problem& p) {
   return DSPARK_OK;
 }
 
-int validate(const dspark_qmm_problem* problems, int count, int64_t M, int bits, int group_size, long* Ns) {
+int validate(const dspark_qmm_problem* problems, int count, int64_t M, int bits, int group_size, long* Ns,
+             bool packed = false) {
   if (!problems || count < 1 || count > kQmmMaxProblems)
     return fail(DSPARK_ERR_ARG, "qmm: problem count %d (1..%d)", count, kQmmMaxProblems);
   for (int i = 0; i < count; ++i) {
     int st = check_common(M, problems[i].K, problems[i].N, bits, group_size);
     if (st) return st;
+    if (packed && problems[i].K % 512)
+      return fail(DSPARK_ERR_SHAPE, "qmm_packed: K=%lld is not a multiple of 512", (long long)problems[i].K);
     if ((st = check_problem(problems[i]))) return st;
     if (problems[i].K != problems[0].K) return fail(DSPARK_ERR_SHAPE, "qmm: all problems of one launch must share K");
     Ns[i] = problems[i].N;
@@ -173,11 +240,14 @@ extern "C" size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, i
   return p.ctr_bytes + p.part_bytes;
 }
 
-extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int count, int64_t M, int bits,
-                                       int group_size, void* workspace, size_t workspace_bytes,
-                                       dspark_stream stream) {
+namespace dspark {
+namespace {
+// One launch over `count` problems; problems[i].w / .scales / .biases are the reference layout,
+// or (packed) the tile stream / the scale-bias tiles / unused.
+int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bits, int group_size, bool packed,
+               void* workspace, size_t workspace_bytes, hipStream_t s) {
   long Ns[kQmmMaxProblems];
-  int st = validate(problems, count, M, bits, group_size, Ns);
+  int st = validate(problems, count, M, bits, group_size, Ns, packed);
   if (st) return st;
   const long K = problems[0].K;
   const Plan p = make_plan(Ns, count, K, M, bits);
@@ -218,14 +288,94 @@ extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int c
       part += (size_t)d.strips * p.mtiles * p.S * 16 * kStripRows;
     }
     strip0 += d.strips;
-    sbvec = sbvec && aligned(q.scales, 16) && aligned(q.biases, 16);
+    if (!packed) sbvec = sbvec && aligned(q.scales, 16) && aligned(q.biases, 16);
   }
   for (int i = count; i < kQmmMaxProblems; ++i) {
     a.p[i] = a.p[0];
     a.p[i].strip0 = 1 << 30;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (packed) return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
   return bits == 4 ? launch_bits<4>(a, p, sbvec, s) : launch_bits<8>(a, p, sbvec, s);
+}
+
+int to_views(const dspark_qmm_packed_problem* pp, int count, dspark_qmm_problem* out) {
+  if (!pp || count < 1 || count > kQmmMaxProblems)
+    return fail(DSPARK_ERR_ARG, "qmm_packed: problem count %d (1..%d)", count, kQmmMaxProblems);
+  for (int i = 0; i < count; ++i) {
+    out[i].x = pp[i].x;
+    out[i].ldx = pp[i].ldx;
+    out[i].w = static_cast<const uint32_t*>(pp[i].packed);
+    out[i].scales = nullptr;  // set once bits are known
+    out[i].biases = nullptr;
+    out[i].y = pp[i].y;
+    out[i].ldy = pp[i].ldy;
+    out[i].N = pp[i].N;
+    out[i].K = pp[i].K;
+  }
+  return DSPARK_OK;
+}
+
+int packed_views(const dspark_qmm_packed_problem* pp, int count, int bits, dspark_qmm_problem* out) {
+  int st = to_views(pp, count, out);
+  if (st) return st;
+  for (int i = 0; i < count; ++i) {
+    if (!pp[i].packed) return fail(DSPARK_ERR_ARG, "qmm_packed: null packed pointer");
+    if (!aligned(pp[i].packed, 16)) return fail(DSPARK_ERR_ALIGN, "qmm_packed: packed buffer must be 16-byte aligned");
+    const PackedLayout L = packed_layout(pp[i].N, pp[i].K, bits);
+    out[i].scales = static_cast<const char*>(pp[i].packed) + (size_t)L.wchunks * 16;
+    out[i].biases = out[i].scales;
+  }
+  return DSPARK_OK;
+}
+}  // namespace
+}  // namespace dspark
+
+extern "C" int dspark_qmm_affine_multi(const dspark_qmm_problem* problems, int count, int64_t M, int bits,
+                                       int group_size, void* workspace, size_t workspace_bytes,
+                                       dspark_stream stream) {
+  return multi_impl(problems, count, M, bits, group_size, false, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t dspark_qmm_packed_bytes(int64_t N, int64_t K, int bits, int group_size) {
+  if (check_common(1, K, N, bits, group_size) || K % 512) return 0;
+  return packed_layout(N, K, bits).bytes();
+}
+
+extern "C" int dspark_qmm_pack(const uint32_t* w, const void* scales, const void* biases, int64_t N, int64_t K,
+                               int bits, int group_size, void* packed, size_t packed_bytes, dspark_stream stream) {
+  int st = check_common(1, K, N, bits, group_size);
+  if (st) return st;
+  if (K % 512) return fail(DSPARK_ERR_SHAPE, "qmm_pack: K=%lld is not a multiple of 512", (long long)K);
+  if (!w || !scales || !biases || !packed) return fail(DSPARK_ERR_ARG, "qmm_pack: null pointer");
+  if (!aligned(w, 16) || !aligned(scales, 16) || !aligned(biases, 16) || !aligned(packed, 16))
+    return fail(DSPARK_ERR_ALIGN, "qmm_pack: weights, scales, biases and the packed buffer must be 16-byte aligned");
+  const PackedLayout L = packed_layout(N, K, bits);
+  if (packed_bytes < L.bytes())
+    return fail(DSPARK_ERR_WORKSPACE, "qmm_pack: packed buffer %zu < %zu bytes", packed_bytes, L.bytes());
+  const long chunks = L.wchunks + L.schunks;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), reinterpret_cast<const unsigned char*>(w),
+                     static_cast<const u16*>(scales), static_cast<const u16*>(biases), (long)N, (int)K, bits,
+                     L.wchunks, L.schunks, static_cast<unsigned char*>(packed));
+  return check_launch("dspark_qmm_pack");
+}
+
+extern "C" int dspark_qmm_packed_multi(const dspark_qmm_packed_problem* problems, int count, int64_t M, int bits,
+                                       int group_size, void* workspace, size_t workspace_bytes,
+                                       dspark_stream stream) {
+  dspark_qmm_problem views[kQmmMaxProblems];
+  int st = packed_views(problems, count, bits, views);
+  if (st) return st;
+  return multi_impl(views, count, M, bits, group_size, true, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t dspark_qmm_packed_multi_workspace(const dspark_qmm_packed_problem* problems, int count, int64_t M,
+                                                    int bits, int group_size) {
+  dspark_qmm_problem views[kQmmMaxProblems];
+  if (packed_views(problems, count, bits, views)) return 0;
+  return dspark_qmm_affine_multi_workspace(views, count, M, bits, group_size);
 }
 
 extern "C" int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t K, const uint32_t* w,

@@ -155,8 +155,12 @@ __device__ __forceinline__ void group_fma(u32x4_t a0, u32x4_t a1, f32x4_t c, u32
   for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(bm, c[r], __builtin_fmaf(sf, p[r], acc[r]));
 }
 
-template <int BITS, int NS, int KSMAX, bool SBVEC>
+// PACKED: the weights and scales/biases come in the tiled form dspark_qmm_pack writes (see
+// pack_* below): P.w is the tile stream, P.s the scale/bias tiles (P.b unused); requires
+// SBVEC (G % 8 == 0). Same products, bit for bit, as the reference layout.
+template <int BITS, int NS, int KSMAX, bool SBVEC, bool PACKED = false>
 __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
+  static_assert(!PACKED || SBVEC, "the packed form needs 8-group slices");
   constexpr int XP = KSMAX * 64 + 8;  // LDS row pitch of the staged x slice (elements)
   __shared__ __attribute__((aligned(16))) u16 xs[16 * XP];
   // per group: 16 row sums (8-bit: sum x; 4-bit: -128 * sum x, the MFMA seed)
@@ -165,7 +169,8 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   // SBVEC: scales (0) and biases (1) of the strip's 16*NS rows over the slice, row pitch
   // SBP (16-byte rows; 4-byte reads of 16 consecutive rows fall in distinct banks)
   constexpr int SBP = KSMAX + 8;
-  __shared__ __attribute__((aligned(16))) u16 sbl[SBVEC ? 2 : 1][SBVEC ? 16 * NS : 1][SBVEC ? SBP : 1];
+  constexpr bool SBLDS = SBVEC && !PACKED;
+  __shared__ __attribute__((aligned(16))) u16 sbl[SBLDS ? 2 : 1][SBLDS ? 16 * NS : 1][SBLDS ? SBP : 1];
 
   const int bx = blockIdx.x;
   int pi = 0;
@@ -213,11 +218,22 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   // ---- 2. scales / biases of the strip's rows over the slice. SBVEC (G a multiple of 8, so
   // slices are too; 16-byte aligned arrays): the workgroup reads them as 16-byte chunks,
   // one (array, row, 8 groups) each, into LDS. Otherwise every lane reads its own row's.
-  constexpr int SBCH = SBVEC ? (2 * 16 * NS * (KSMAX / 8) + 64 * NS - 1) / (64 * NS) : 1;
+  constexpr int SBCH = SBLDS ? (2 * 16 * NS * (KSMAX / 8) + 64 * NS - 1) / (64 * NS) : 1;
   u32x4_t sbv[SBCH];
   u32 svs[SBVEC ? 1 : KSMAX], bvs[SBVEC ? 1 : KSMAX];
+  u32x4_t tsv[PACKED ? KSMAX / 8 : 1], tbv[PACKED ? KSMAX / 8 : 1];  // packed: 8 groups per load
   const int cpa = 16 * NS * (gcount >> 3);  // chunks per array
-  if constexpr (SBVEC) {
+  const long tile16 = n >> 4;                 // packed: this wave's 16-row tile
+  if constexpr (PACKED) {
+    // tile (t, octet j): 256 B of scales then 256 B of biases, row r at 16 r
+#pragma unroll
+    for (int j = 0; j < KSMAX / 8; ++j) {
+      const int jj = min(j, (gcount >> 3) - 1);
+      const u16* blk = P.s + ((tile16 * (G >> 3) + (gs >> 3) + jj) * 2) * 128 + 8 * c16;
+      tsv[j] = ldg128(blk);
+      tbv[j] = ldg128(blk + 128);
+    }
+  } else if constexpr (SBVEC) {
 #pragma unroll
     for (int j = 0; j < SBCH; ++j) {
       const int ci = min(tid + 64 * NS * j, 2 * cpa - 1);
@@ -237,7 +253,18 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   }
   // ---- 3. every weight load of this lane's row in the slice (clamped, unconditional)
   WSlice<BITS, KSMAX> wsl;
-  wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
+  if constexpr (PACKED) {
+    // tile stream: 1 KB per (16-row tile, group) for 8-bit, per (tile, group pair) for 4-bit,
+    // lane l's 16 bytes at 16 l, already in the order the MFMA B operand takes
+    constexpr int NL = BITS == 4 ? KSMAX / 2 : KSMAX;
+    const int per_tile = BITS == 4 ? (G >> 1) : G, first = BITS == 4 ? (gs >> 1) : gs;
+    const int nl = BITS == 4 ? (gcount >> 1) : gcount;
+    const char* tb = reinterpret_cast<const char*>(P.w) + ((tile16 * per_tile + first) * 64 + lane) * 16;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) wsl.v[j] = ldg128(tb + (long)min(j, nl - 1) * 1024);
+  } else {
+    wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
+  }
   // every load above is issued before anything consumes one (keeps the scheduler from
   // interleaving the x processing, and its waits, into the load sequence)
   __builtin_amdgcn_sched_barrier(0);
@@ -260,7 +287,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     *reinterpret_cast<u32x4_t*>(&xs[row * XP + (valid ? 8 * col : KSMAX * 64)]) = v;
     if (valid && (c & 7) == 0) xsum[(col >> 3) * 16 + row] = s8;
   }
-  if constexpr (SBVEC) {
+  if constexpr (SBLDS) {
 #pragma unroll
     for (int j = 0; j < SBCH; ++j) {
       const int ci = tid + 64 * NS * j;
@@ -280,9 +307,19 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   for (int gl = 0; gl < KSMAX; gl += 2) {
     if (gl >= gcount) break;
     u32x2_t w4[2] = {};
-    if constexpr (BITS == 4) frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
+    if constexpr (BITS == 4) {
+      if constexpr (PACKED) {
+        w4[0] = u32x2_t{wsl.v[gl >> 1].x, wsl.v[gl >> 1].y};
+        w4[1] = u32x2_t{wsl.v[gl >> 1].z, wsl.v[gl >> 1].w};
+      } else {
+        frag_u4(wsl.v[gl >> 1], w4[0], w4[1]);
+      }
+    }
     u32 s2 = 0, b2 = 0;
-    if constexpr (SBVEC) {
+    if constexpr (PACKED) {
+      s2 = tsv[gl >> 3][(gl & 7) >> 1];
+      b2 = tbv[gl >> 3][(gl & 7) >> 1];
+    } else if constexpr (SBVEC) {
       s2 = *reinterpret_cast<const u32*>(&sbl[0][srow_l][gl]);
       b2 = *reinterpret_cast<const u32*>(&sbl[1][srow_l][gl]);
     }

@@ -62,6 +62,20 @@ class QmmProblem(ctypes.Structure):
     ]
 
 
+class QmmPackedProblem(ctypes.Structure):
+    """``dspark_qmm_packed_problem`` (include/dspark.h)."""
+
+    _fields_ = [
+        ("x", c_void_p),
+        ("ldx", c_i64),
+        ("packed", c_void_p),
+        ("y", c_void_p),
+        ("ldy", c_i64),
+        ("N", c_i64),
+        ("K", c_i64),
+    ]
+
+
 MAX_QMM_PROBLEMS = 4
 
 # name -> (restype, argtypes). Every symbol include/dspark.h declares.
@@ -76,6 +90,13 @@ SIGNATURES: dict[str, tuple] = {
     "dspark_qmm_affine_multi": (c_int, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int, c_void_p,
                                         c_size_t, c_void_p]),
     "dspark_qmm_affine_multi_workspace": (c_size_t, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int]),
+    "dspark_qmm_packed_bytes": (c_size_t, [c_i64, c_i64, c_int, c_int]),
+    "dspark_qmm_pack": (c_int, [c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_int, c_int, c_void_p, c_size_t,
+                                c_void_p]),
+    "dspark_qmm_packed_multi": (c_int, [ctypes.POINTER(QmmPackedProblem), c_int, c_i64, c_int, c_int, c_void_p,
+                                        c_size_t, c_void_p]),
+    "dspark_qmm_packed_multi_workspace": (c_size_t, [ctypes.POINTER(QmmPackedProblem), c_int, c_i64, c_int,
+                                                     c_int]),
     "dspark_verify_attention": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_i64_p,
                                         c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                         c_size_t, c_void_p]),

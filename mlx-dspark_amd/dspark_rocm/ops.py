@@ -129,6 +129,83 @@ def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = 
     return results
 
 
+class PackedQmm:
+    """A quantized [N, K] matrix in the MI355X packed form (``dspark_qmm_pack``): 16-row weight
+    tiles in the MFMA lane order plus 16-row x 8-group scale/bias tiles, in one uint8 buffer.
+    Products equal those of the reference layout bit for bit."""
+
+    def __init__(self, buf: torch.Tensor, n: int, k: int, bits: int):
+        self.buf, self.n, self.k, self.bits = buf, n, k, bits
+
+    @property
+    def nbytes(self) -> int:
+        return self.buf.numel()
+
+
+def qmm_packable(n: int, k: int, bits: int, group_size: int = GROUP) -> bool:
+    """True when ``dspark_qmm_pack`` accepts [n, k] (K % 512 == 0, 4/8-bit, groups of 64)."""
+    return int(_lib.load().dspark_qmm_packed_bytes(n, k, bits, group_size)) > 0
+
+
+def qmm_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, bits: int,
+             group_size: int = GROUP) -> PackedQmm:
+    """Pack the reference layout (uint32 [N, K*bits/32], bf16 scales/biases [N, K/64]) once."""
+    _require_cuda(w, scales, biases)
+    _require_packed(w)
+    n, k = w.shape[0], w.shape[1] * 32 // bits
+    w, scales, biases = w.contiguous(), scales.contiguous(), biases.contiguous()
+    lib = _lib.load()
+    nbytes = int(lib.dspark_qmm_packed_bytes(n, k, bits, group_size))
+    if nbytes == 0:
+        raise _lib.DsparkError("dspark_qmm_pack", -2, f"[{n}, {k}] {bits}-bit cannot be packed (K % 512 != 0)")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _lib.call("dspark_qmm_pack", _ptr(w), _ptr(scales), _ptr(biases), n, k, bits, group_size, _ptr(buf), nbytes,
+              _stream(w))
+    return PackedQmm(buf, n, k, bits)
+
+
+def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROUP, outs=None) -> list[torch.Tensor]:
+    """``quantized_matmul_multi`` over packed matrices (one launch, same M, K and bits)."""
+    cnt = len(packed_list)
+    if not 1 <= cnt <= _lib.MAX_QMM_PROBLEMS:
+        raise ValueError(f"1..{_lib.MAX_QMM_PROBLEMS} problems per launch, got {cnt}")
+    if len(x_list) == 1 and cnt > 1:
+        x_list = list(x_list) * cnt
+    bits = packed_list[0].bits
+    probs = (_lib.QmmPackedProblem * cnt)()
+    results, keep, m = [], [], None
+    for i in range(cnt):
+        x, pq = x_list[i], packed_list[i]
+        _require_cuda(x, pq.buf)
+        _require_bf16("x", x)
+        if pq.bits != bits:
+            raise ValueError("all packed problems of one launch must share bits")
+        k = x.shape[-1]
+        if k != pq.k:
+            raise ValueError(f"x has K={k}, the packed matrix K={pq.k}")
+        x2 = x.reshape(-1, k)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        if m is None:
+            m = x2.shape[0]
+        elif x2.shape[0] != m:
+            raise ValueError("all problems must have the same number of rows")
+        y = outs[i] if outs is not None else torch.empty((m, pq.n), dtype=torch.bfloat16, device=x.device)
+        keep += [x2, y]
+        probs[i] = _lib.QmmPackedProblem(_ptr(x2), x2.stride(0), _ptr(pq.buf), _ptr(y), y.stride(0), pq.n, k)
+        results.append(y.reshape(*x.shape[:-1], pq.n))
+    nbytes = _lib.load().dspark_qmm_packed_multi_workspace(probs, cnt, m, bits, group_size)
+    ws = qmm_workspace(x_list[0].device, nbytes)
+    _lib.call("dspark_qmm_packed_multi", probs, cnt, m, bits, group_size, _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(x_list[0]))
+    return results
+
+
+def quantized_matmul_packed(x: torch.Tensor, packed: PackedQmm, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x [.., K] @ dequant(W)^T`` for a packed W -> ``[.., N]`` bf16."""
+    return quantized_matmul_packed_multi([x], [packed], outs=None if out is None else [out])[0]
+
+
 def qmm_supported(m: int, k: int, n: int, bits: int, group_size: int = GROUP) -> bool:
     return _lib.load().dspark_qmm_affine_supported(m, k, n, bits, group_size) == 0
 

@@ -1,0 +1,124 @@
+"""GPU: the MI355X packed qmm form (dspark_qmm_pack / dspark_qmm_packed_multi).
+
+- The packed bytes equal a numpy restatement of the layout definition (include/dspark.h,
+  csrc/dspark_qmm.hip `pack_kernel`): 16-row weight tiles in MFMA lane order, then 16-row x
+  8-group scale/bias tiles, rows past N zero.
+- Every product equals the reference-layout kernel's bit for bit (same slices, same per-group
+  arithmetic and order), over 4/8 bits, N not a multiple of 16, M = 1..33, multi-problem
+  launches; and both are held to the oracle at the qmm bar.
+"""
+
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import pytest
+
+from _util import assert_rms_close, from_dev_bf16, randn_bf16, rng, to_dev_bf16, to_dev_packed
+from oracle import qmm_ref, quant_ref
+
+pytestmark = pytest.mark.gpu
+
+
+@functools.lru_cache(maxsize=8)
+def _quantized(seed, n, k, bits):
+    r = rng(seed)
+    w = randn_bf16(r, n, k)
+    return quant_ref.quantize(w, bits=bits)          # (packed uint32 [n, k*bits/32], scales, biases)
+
+
+def _pack_np(wq: np.ndarray, s: np.ndarray, b: np.ndarray, n: int, k: int, bits: int) -> np.ndarray:
+    """The packed layout from its definition, with plain numpy indexing."""
+    g = k // 64
+    t = (n + 15) // 16
+    wb = np.ascontiguousarray(wq).view(np.uint8).reshape(n, k * bits // 8)
+    sb = np.asarray(quant_ref.bf16_bits(s), dtype=np.uint16).reshape(n, g)
+    bb = np.asarray(quant_ref.bf16_bits(b), dtype=np.uint16).reshape(n, g)
+    rows = np.zeros((t * 16, wb.shape[1]), dtype=np.uint8)
+    rows[:n] = wb
+    srows = np.zeros((t * 16, g), dtype=np.uint16)
+    brows = np.zeros((t * 16, g), dtype=np.uint16)
+    srows[:n], brows[:n] = sb, bb
+    out = []
+    per_tile = g // 2 if bits == 4 else g
+    for ti in range(t):
+        for j in range(per_tile):
+            for lane in range(64):
+                r, q = 16 * ti + (lane & 15), lane >> 4
+                if bits == 8:
+                    out.append(rows[r, 64 * j + 16 * q: 64 * j + 16 * q + 16])
+                else:
+                    qs = 2 * (q & 1) + (q >> 1)
+                    out.append(np.concatenate([rows[r, 32 * (2 * j) + 8 * qs: 32 * (2 * j) + 8 * qs + 8],
+                                               rows[r, 32 * (2 * j + 1) + 8 * qs: 32 * (2 * j + 1) + 8 * qs + 8]]))
+    for ti in range(t):
+        for o in range(g // 8):
+            for arr in (srows, brows):
+                for r16 in range(16):
+                    out.append(arr[16 * ti + r16, 8 * o: 8 * o + 8].view(np.uint8))
+    return np.concatenate(out)
+
+
+def _dev(wq, s, b, dev):
+    return to_dev_packed(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+
+
+@pytest.mark.parametrize("n,k,bits", [(40, 512, 8), (40, 1024, 4), (16, 512, 4)])
+def test_layout_matches_definition(dev, n, k, bits):
+    from dspark_rocm import ops
+
+    wq, s, b = _quantized(n + k + bits, n, k, bits)
+    pq = ops.qmm_pack(*_dev(wq, s, b, dev), bits=bits)
+    got = pq.buf.cpu().numpy()
+    want = _pack_np(wq, s, b, n, k, bits)
+    assert got.shape == want.shape
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("n,k", [(1000, 512), (4096, 4096), (520, 5120), (64, 25600)])
+@pytest.mark.parametrize("m", [1, 5, 16, 33])
+def test_bit_identical_to_reference_layout(dev, bits, n, k, m):
+    import torch
+
+    from dspark_rocm import ops
+
+    wq, s, b = _quantized(7 * n + k + bits, n, k, bits)
+    wd, sd, bd = _dev(wq, s, b, dev)
+    x = randn_bf16(rng(m + n), m, k)
+    xd = to_dev_bf16(x, dev)
+    ref_layout = ops.quantized_matmul(xd, wd, sd, bd, bits=bits)
+    packed = ops.quantized_matmul_packed(xd, ops.qmm_pack(wd, sd, bd, bits=bits))
+    assert torch.equal(packed, ref_layout)
+    if n * k <= 4096 * 4096 and m <= 16:
+        want = qmm_ref.qmm_f64(x, wq, s, b, bits)
+        assert_rms_close(from_dev_bf16(packed), want, 2e-2, f"packed {bits}-bit [{n},{k}] M={m}")
+
+
+def test_multi_equals_single(dev):
+    import torch
+
+    from dspark_rocm import ops
+
+    k, bits = 4096, 8
+    mats = [_dev(*_quantized(i, n, k, bits), dev) for i, n in enumerate((4096, 1024, 1024))]
+    packs = [ops.qmm_pack(*m, bits=bits) for m in mats]
+    x = to_dev_bf16(randn_bf16(rng(3), 16, k), dev)
+    multi = ops.quantized_matmul_packed_multi([x], packs)
+    for pq, (wd, sd, bd), y in zip(packs, mats, multi):
+        assert torch.equal(y, ops.quantized_matmul_packed(x, pq))
+        assert torch.equal(y, ops.quantized_matmul(x, wd, sd, bd, bits=bits))
+
+
+def test_refusals(dev):
+    import torch
+
+    from dspark_rocm import _lib, ops
+
+    assert not ops.qmm_packable(64, 448, 8)          # K % 512 != 0
+    assert ops.qmm_packable(64, 512, 4)
+    w = torch.zeros((64, 448 // 4), dtype=torch.int32, device=dev)
+    s = torch.zeros((64, 7), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_lib.DsparkError):
+        ops.qmm_pack(w, s, s, bits=8)
