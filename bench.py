@@ -99,7 +99,9 @@ def time_eager(fn, reps: int, warm: int = 3) -> float:
 # ------------------------------------------------------------------ workloads
 
 class LayerSet:
-    """C2: q/k/v/o/gate/up/down of an 8B-shaped layer, 8-bit g64, M rows; a pool of layers."""
+    """C2: q/k/v/o/gate/up/down of an 8B-shaped layer, 8-bit g64, M rows; a pool of layers.
+    Each matrix is held in the reference layout and in the packed qmm form (``ops.qmm_pack``);
+    ``packed`` selects which one the launches read (the products are bit-identical)."""
 
     H, HQ, HK, D, I = 4096, 32, 8, 128, 12288
 
@@ -119,6 +121,10 @@ class LayerSet:
         for _ in range(layers):
             self.layers.append({name: random_quantized(n, k, bits, generator=g, device=dev)
                                 for name, (n, k) in shapes.items()})
+        from dspark_rocm import ops
+
+        self.packs = [{name: ops.qmm_pack(*L[name], bits=bits) for name in shapes} for L in self.layers]
+        self.packed = True
         self.x = {k: (torch.randn((m, kk), generator=g, device=dev) ).to(torch.bfloat16)
                   for k, kk in (("qkv", H), ("o", self.HQ * D), ("gu", H), ("down", I))}
         self.y = {name: torch.empty((m, n), dtype=torch.bfloat16, device=dev) for name, (n, _) in shapes.items()}
@@ -130,16 +136,27 @@ class LayerSet:
         """The step's dominant launch: gate and up projections as one two-problem qmm launch."""
         from dspark_rocm import ops
 
-        L = self.layers[i % len(self.layers)]
         x, y = self.x, self.y
+        if self.packed:
+            P = self.packs[i % len(self.packs)]
+            ops.quantized_matmul_packed_multi([x["gu"]], [P["gate"], P["up"]], outs=[y["gate"], y["up"]])
+            return
+        L = self.layers[i % len(self.layers)]
         ops.quantized_matmul_multi([x["gu"]], [L["gate"][0], L["up"][0]], [L["gate"][1], L["up"][1]],
                                    [L["gate"][2], L["up"][2]], bits=self.bits, outs=[y["gate"], y["up"]])
 
     def step(self, i: int) -> None:
         from dspark_rocm import ops
 
-        L = self.layers[i % len(self.layers)]
         b, y, x = self.bits, self.y, self.x
+        if self.packed:
+            P = self.packs[i % len(self.packs)]
+            ops.quantized_matmul_packed_multi([x["qkv"]], [P[n] for n in "qkv"], outs=[y["q"], y["k"], y["v"]])
+            ops.quantized_matmul_packed(x["o"], P["o"], out=y["o"])
+            self.gate_up(i)
+            ops.quantized_matmul_packed(x["down"], P["down"], out=y["down"])
+            return
+        L = self.layers[i % len(self.layers)]
         ops.quantized_matmul_multi([x["qkv"]], [L[n][0] for n in "qkv"], [L[n][1] for n in "qkv"],
                                    [L[n][2] for n in "qkv"], bits=b, outs=[y["q"], y["k"], y["v"]])
         ops.quantized_matmul(x["o"], *L["o"], bits=b, out=y["o"])
@@ -429,7 +446,8 @@ def main() -> None:
         f"({time.perf_counter() - t0:.1f} s)")
 
     traffic = load_traffic()
-    roofline = {"kernel": "qmm_sk_kernel<8,4,16,true> gate+up launch (N=2x12288, K=4096, M=16; grid 384x4)", "bound": "hbm",
+    roofline = {"kernel": "qmm_sk_kernel<8,4,16,true,true> gate+up launch, packed form (N=2x12288, K=4096, M=16; "
+                          "grid 384x4)", "bound": "hbm",
                 "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                 "traffic": (traffic or {}).get("qmm_gate_up_bytes"),
@@ -438,6 +456,15 @@ def main() -> None:
     extra = {"C2_step_us": round(ms_step * 1e3, 3), "C2_eager_step_us": round(eager_ms * 1e3, 3),
              "C2_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if not a.quick:
+        # the same set read from the reference layout (what a drop-in caller passes per call)
+        ls.packed = False
+        ref_ms, _ = time_graph(lambda: [ls.step(i) for i in range(K)], 1)
+        ref_gu, _ = time_graph(lambda: [ls.gate_up(i) for i in range(K)], 1)
+        ls.packed = True
+        extra["C2_reference_layout"] = {"step_us": round(ref_ms * 1e3 / K, 3),
+                                        "GBs": round(ls.bytes_per_step / (ref_ms / K * 1e-3) / 1e9, 1),
+                                        "gate_up_us": round(ref_gu * 1e3 / K, 3)}
+        log(f"C2 reference layout: {ref_ms * 1e3 / K:.2f} us/step, gate/up {ref_gu * 1e3 / K:.2f} us")
         extra["C1"] = []
         for b in (4, 8):
             for m in (1, 2, 4, 8, 16):
@@ -470,7 +497,8 @@ def main() -> None:
             "dtype": "bf16", "data": "synthetic",
             "config": {"workload": "8B-shaped 8-bit layer projection set (q,k,v,o,gate,up,down; hidden 4096, "
                                    "heads 32/8x128, intermediate 12288, group 64) at M=16 verify rows, "
-                                   f"rotated over {a.layers} distinct layers", "M": M, "bits": bits,
+                                   f"rotated over {a.layers} distinct layers, weights in the packed qmm form",
+                       "M": M, "bits": bits,
                        "bytes_per_step": ls.bytes_per_step, "launches_per_step": 4, "timing": "hipGraph replay"},
             "roofline": roofline, "cpu_baseline": cpu, "extra": extra}
     print(json.dumps(line), flush=True)

@@ -164,11 +164,24 @@ class DenseModel(nn.Module):
 
 
 class VerifyEngine:
-    """Preallocated fused verify step for up to ``max_rows`` rows (batch 1)."""
+    """Preallocated fused verify step for up to ``max_rows`` rows (batch 1). With ``packed``,
+    every projection whose K is a multiple of 512 is held (also) in the MI355X packed qmm form
+    (``ops.qmm_pack``, packed once here) and multiplied from it; products are bit-identical to
+    the reference layout's."""
 
-    def __init__(self, model: DenseModel, max_rows: int = 16):
+    def __init__(self, model: DenseModel, max_rows: int = 16, packed: bool = True):
         a = model.args
         self.model, self.args, self.max_rows = model, a, max_rows
+        self._packed: dict[int, ops.PackedQmm] = {}
+        if packed:
+            mods = [model.lm_head]
+            for layer in model.layers:
+                at, mlp = layer.self_attn, layer.mlp
+                mods += [at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj]
+            for mod in mods:
+                n, k = mod.weight.shape[0], mod.weight.shape[1] * 32 // mod.bits
+                if ops.qmm_packable(n, k, mod.bits):
+                    self._packed[id(mod)] = ops.qmm_pack(mod.weight, mod.scales, mod.biases, bits=mod.bits)
         dev = model.embed_tokens.device
         H, I, hq, hk, d = (a.hidden_size, a.intermediate_size, a.num_attention_heads, a.num_key_value_heads,
                            a.head_dim)
@@ -184,6 +197,15 @@ class VerifyEngine:
         self.tt = torch.zeros(max_rows, dtype=torch.int32, device=dev)
         self.draft = torch.zeros(max(max_rows - 1, 1), dtype=torch.int32, device=dev)
         self.n_acc = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def _qmm(self, x: torch.Tensor, mods, outs) -> None:
+        """One launch of ``x @ W^T`` for the modules ``mods`` (same K and bits) into ``outs``."""
+        packs = [self._packed.get(id(mod)) for mod in mods]
+        if all(p is not None for p in packs):
+            ops.quantized_matmul_packed_multi([x], packs, outs=outs)
+        else:
+            ops.quantized_matmul_multi([x], [mod.weight for mod in mods], [mod.scales for mod in mods],
+                                       [mod.biases for mod in mods], bits=mods[0].bits, outs=outs)
 
     def step(self, M: int, cache: list[KVCache], pos0: int, *, accept: bool = False) -> torch.Tensor:
         """Run the forward over ``self.ids[:M]`` at cache positions pos0..pos0+M-1 (caches
@@ -204,29 +226,22 @@ class VerifyEngine:
                 ops.rmsnorm(h, layer.input_layernorm, eps, out=y)
             else:
                 ops.rmsnorm(h, layer.input_layernorm, eps, residual=r, h_out=h, out=y)
-            ops.quantized_matmul_multi([y], [at.q_proj.weight, at.k_proj.weight, at.v_proj.weight],
-                                       [at.q_proj.scales, at.k_proj.scales, at.v_proj.scales],
-                                       [at.q_proj.biases, at.k_proj.biases, at.v_proj.biases], bits=at.q_proj.bits,
-                                       outs=[self.q[:M], self.k[:M], self.v[:M]])
+            self._qmm(y, [at.q_proj, at.k_proj, at.v_proj], [self.q[:M], self.k[:M], self.v[:M]])
             ops.qk_norm_rope_kv(self.q[:M], self.k[:M], self.v[:M], at.q_norm, at.k_norm, heads=hq, kv_heads=hk,
                                 head_dim=d, eps=eps, rope_base=a.rope_theta, pos0=pos0, q_out=qatt[0],
                                 k_cache=c.keys[0], v_cache=c.values[0])
             kv, vv = c.keys[:, :, :L], c.values[:, :, :L]
             att = self.att[:M]
             ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1)
-            ops.quantized_matmul(att, at.o_proj.weight, at.o_proj.scales, at.o_proj.biases, bits=at.o_proj.bits, out=r)
+            self._qmm(att, [at.o_proj], [r])
             ops.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
-            ops.quantized_matmul_multi([y], [mlp.gate_proj.weight, mlp.up_proj.weight],
-                                       [mlp.gate_proj.scales, mlp.up_proj.scales],
-                                       [mlp.gate_proj.biases, mlp.up_proj.biases], bits=mlp.gate_proj.bits,
-                                       outs=[self.g[:M], self.u[:M]])
+            self._qmm(y, [mlp.gate_proj, mlp.up_proj], [self.g[:M], self.u[:M]])
             ops.swiglu(self.g[:M], self.u[:M], out=self.hm[:M])
-            ops.quantized_matmul(self.hm[:M], mlp.down_proj.weight, mlp.down_proj.scales, mlp.down_proj.biases,
-                                 bits=mlp.down_proj.bits, out=r)
+            self._qmm(self.hm[:M], [mlp.down_proj], [r])
         ops.rmsnorm(h, m.norm, eps, residual=r, h_out=h, out=y)
         lm = m.lm_head
         logits = self.logits[:M]
-        ops.quantized_matmul(y, lm.weight, lm.scales, lm.biases, bits=lm.bits, out=logits)
+        self._qmm(y, [lm], [logits])
         if accept:
             ops.argmax_rows(logits, out=self.tt[:M])
             ops.greedy_accept(self.draft[:M - 1], self.tt[:M], out=self.n_acc)
@@ -237,9 +252,9 @@ class Target:
     """The reference's Target surface for a dense model: ``make_cache``, ``verify``,
     ``plain``, ``rollback`` (target.py:166-184, :642-696), plus the greedy round."""
 
-    def __init__(self, model: DenseModel, max_rows: int = 16):
+    def __init__(self, model: DenseModel, max_rows: int = 16, packed: bool = True):
         self.model = model
-        self.engine = VerifyEngine(model, max_rows)
+        self.engine = VerifyEngine(model, max_rows, packed=packed)
         self.max_rows = max_rows
 
     def make_cache(self, capacity: int = 0) -> list[KVCache]:

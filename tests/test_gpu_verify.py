@@ -182,3 +182,24 @@ def test_speculative_trace_is_lossless_with_expected_accept_length(dev):
     assert out[:steps] == greedy[:steps]
     # the first token came from the prompt's forward; the rounds committed the rest
     assert verify_ref.mean_accept_len(sum(expected_acc), rounds) == (len(out) - 1) / rounds
+
+
+def test_packed_engine_is_bitwise_the_reference_layout_engine(dev):
+    """The fused step reading every projection from the packed qmm form (hidden 512 and
+    intermediate 1024, so all seven projections and the lm_head are packable) produces the same
+    logits, bit for bit, as the step reading the reference layout, over blocks with rollback."""
+    from dspark_rocm.model import Target
+
+    model = tiny_model(dev, seed=9, hidden_size=512, intermediate_size=1024)
+    packed, plain = Target(model, packed=True), Target(model, packed=False)
+    n_mods = 7 * model.args.num_hidden_layers + 1
+    assert len(packed.engine._packed) == n_mods and not plain.engine._packed
+    ca, cb = packed.make_cache(96), plain.make_cache(96)
+    r = np.random.Generator(np.random.PCG64(4))
+    for n, rej in ((16, 3), (7, 0), (16, 15)):
+        ids = torch.tensor([r.integers(0, 512, n).tolist()])
+        la, _ = packed.verify(ids, ca)
+        lb, _ = plain.verify(ids, cb)
+        assert torch.equal(la, lb)
+        packed.rollback(ca, rej)
+        plain.rollback(cb, rej)
