@@ -36,6 +36,9 @@ HIPCC_FLAGS = [
     f"-I{CSRC}",
     # no packed fp32 arithmetic in device code (v_pk_{add,mul,fma}_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: accumulator registers would cost a v_accvgpr move per
+    # value on every rescale / scale-FMA (and an occupancy step for the 4-wave attention)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -12,10 +12,11 @@
 //   * grid = (B*Hk, NB key blocks, row groups); a workgroup of 4 or 8 waves owns one KV
 //     head's key block and up to 4 or 8 row tiles of 16 rows (all gqa*Mq rows of the head
 //     when there are at most 128), so each K/V byte is read from HBM once and shared by every
-//     query head of the GQA group.
-//   * 64-key tiles are staged through LDS with register double buffering: K row-major
-//     (padded rows), V transposed (key-contiguous, 8-key blocks XOR-swizzled by d) because the
-//     P.V MFMA reduces over keys.
+//     query head of the GQA group. On short caches (few blocks) the 4 row tiles are worked by
+//     8 waves, two per tile splitting its keys.
+//   * 64-key tiles are staged through LDS from registers loaded one (4-wave workgroups) or two
+//     (8-wave workgroups) tiles ahead: K row-major (padded rows), V transposed (key-contiguous,
+//     8-key blocks XOR-swizzled by d) because the P.V MFMA reduces over keys.
 //   * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16. Computing the transposed
 //     scores leaves each lane holding 8 keys of one query row, which is exactly the B operand
 //     of the P.V MFMA — no shuffle of P.
@@ -60,26 +61,36 @@ __device__ __forceinline__ int vt_off(int d, int pos) {
   return d * KT + ((((pos >> 3) ^ (d >> 1) ^ (d >> 3)) & 7) << 3) + (pos & 7);
 }
 
-// WV waves = WV row tiles per workgroup (4, or 8 when a KV head has more than 4 row tiles, so
-// every row of the head shares one read of each K/V tile).
-template <int D, bool TREE, int WV>
-__global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
-  constexpr int THREADS = 64 * WV;
+// WV row tiles per workgroup (4, or 8 when a KV head has more than 4 row tiles, so every row
+// of the head shares one read of each K/V tile), each worked by KS waves: with KS = 2 wave
+// (tile r, half h) takes keys 32h..32h+31 of every 64-key tile, and the two halves' (m, l, O)
+// are merged in LDS at the end (8 waves per workgroup either way).
+template <int D, bool TREE, int WV, int KS, int PF>
+__global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a) {
+  static_assert(KS == 1 || KS == 2, "key split");
+  static_assert(PF == 1 || PF == 2, "tiles in flight");
+  constexpr int THREADS = 64 * WV * KS;
+  constexpr int NKS = 4 / KS;         // 16-key subtiles of a tile per wave
+  constexpr int NU = 2 / KS;          // 32-key halves of a tile per wave (P.V MFMA k-steps)
   constexpr int KP = D + 8;           // padded K row (elements)
   constexpr int DC = D / 8;           // 16-byte chunks per key row
   constexpr int LOADS = KT * DC / THREADS;  // 16-byte K chunks per thread per tile
   constexpr int NDC = D / 32;         // d-chunks of the S MFMA
   constexpr int NDT = D / 16;         // d-tiles of the O MFMA
-  __shared__ __attribute__((aligned(16))) u16 ks_lds[KT * KP];
-  __shared__ __attribute__((aligned(16))) u16 vt_lds[D * KT];
+  // K tile, then the transposed V tile; reused for the key-half merge after the last tile
+  __shared__ __attribute__((aligned(16))) u16 smem[KT * KP + D * KT];
+  u16* const ks_lds = smem;
+  u16* const vt_lds = smem + KT * KP;
+  static_assert(KS == 1 || (WV * 64 * NDT * 4 + 2 * WV * 16) * 4 <= (KT * KP + D * KT) * 2, "merge area");
 
   const int bh = blockIdx.x;
   const int b = bh / a.Hk, hk = bh % a.Hk;
   const int blk = blockIdx.y;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = uniform(tid >> 6);
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int rt = blockIdx.z * WV + wave;
+  const int rtw = wave % WV, kh = wave / WV;  // row tile in the group, key half
+  const int rt = blockIdx.z * WV + rtw;
   const bool active = rt < a.RT;
 
   const int L = a.L;
@@ -112,19 +123,38 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
   //    their 8 d-rows in pair-swapped order so each half-wave covers all 64 LDS banks.
   const bool vthread = tid < 16 * DC;
   const int vkq = tid & 15, vdc = tid >> 4;
-  u32x4_t kreg[LOADS], vreg[4];
-  auto load_tile = [&](int kt) {
+  struct TileRegs {
+    u32x4_t k[LOADS], v[4];
+  };
+  // A tile inside the cache is addressed as a uniform base (scalar) plus a loop-invariant
+  // 32-bit byte offset per lane; only a tile running past key L - 1 clamps each key.
+  static_assert(THREADS % DC == 0, "K chunks of one thread share their d-chunk");
+  const unsigned koff = (unsigned)(((tid / DC) * a.kss + 8 * (tid % DC)) * 2);
+  const unsigned voff = (unsigned)((4 * vkq * a.vss + 8 * vdc) * 2);
+  const long kstep = (long)(THREADS / DC) * a.kss * 2;  // bytes between a thread's K chunks
+  auto load_tile = [&](TileRegs& r, int kt) {
+    if (kt + KT <= L) {
+      const char* kb = reinterpret_cast<const char*>(kbase + (long)kt * a.kss);
+      const char* vb = reinterpret_cast<const char*>(vbase + (long)kt * a.vss);
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) r.k[j] = ldg128((kb + j * kstep) + koff);
+      if (vthread) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.v[j] = ldg128((vb + (long)j * a.vss * 2) + voff);
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int c = tid + THREADS * j;
       const int key = min(kt + c / DC, L - 1);
-      kreg[j] = ldg128(kbase + (long)key * a.kss + 8 * (c % DC));
+      r.k[j] = ldg128(kbase + (long)key * a.kss + 8 * (c % DC));
     }
     if (vthread) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = min(kt + 4 * vkq + j, L - 1);
-        vreg[j] = ldg128(vbase + (long)key * a.vss + 8 * vdc);
+        r.v[j] = ldg128(vbase + (long)key * a.vss + 8 * vdc);
       }
     }
   };
@@ -133,11 +163,11 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
   const u32 sel_lo = 0x05040100u, sel_hi = 0x07060302u;
   const u32 vsel_even = (vdc & 1) ? sel_hi : sel_lo;  // e even
   const u32 vsel_odd = (vdc & 1) ? sel_lo : sel_hi;   // e odd
-  auto store_tile = [&]() {
+  auto store_tile = [&](const TileRegs& r) {
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int c = tid + THREADS * j;
-      *reinterpret_cast<u32x4_t*>(&ks_lds[(c / DC) * KP + 8 * (c % DC)]) = kreg[j];
+      *reinterpret_cast<u32x4_t*>(&ks_lds[(c / DC) * KP + 8 * (c % DC)]) = r.k[j];
     }
     if (vthread) {
       const int pos = vt_pos(4 * vkq);
@@ -146,30 +176,25 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
         const int d = 8 * vdc + (e ^ (vdc & 1));
         const int wd = e >> 1;
         const u32 vsel = (e & 1) ? vsel_odd : vsel_even;
-        const u32x2_t pr = {__builtin_amdgcn_perm(vreg[1][wd], vreg[0][wd], vsel),
-                            __builtin_amdgcn_perm(vreg[3][wd], vreg[2][wd], vsel)};
+        const u32x2_t pr = {__builtin_amdgcn_perm(r.v[1][wd], r.v[0][wd], vsel),
+                            __builtin_amdgcn_perm(r.v[3][wd], r.v[2][wd], vsel)};
         *reinterpret_cast<u32x2_t*>(&vt_lds[vt_off(d, pos)]) = pr;
       }
     }
   };
 
-  if (k0 < k1) load_tile(k0);
-  for (int kt = k0; kt < k1; kt += KT) {
-    __syncthreads();  // previous tile fully consumed
-    store_tile();
-    __syncthreads();
-    if (kt + KT < k1) load_tile(kt + KT);
-    if (!active) continue;
-
-    // S^T[key][row] for 4 subtiles of 16 keys
-    f32x4_t s[4];
+  auto compute_tile = [&](int kt) {
+    // S^T[key][row] for this wave's NKS subtiles of 16 keys (keys 16 (ks0 + j) ..)
+    const int ks0 = kh * NKS;
+    f32x4_t s[NKS];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      s[ks] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NKS; ++j) {
+      s[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < NDC; ++c) {
-        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(&ks_lds[(16 * ks + c16) * KP + 32 * c + 8 * q4]);
-        s[ks] = mfma16x16x32(kf, qf[c], s[ks]);
+        const u32x4_t kf =
+            *reinterpret_cast<const u32x4_t*>(&ks_lds[(16 * (ks0 + j) + c16) * KP + 32 * c + 8 * q4]);
+        s[j] = mfma16x16x32(kf, qf[c], s[j]);
       }
     }
     // row max of the raw scores (invisible keys -inf; only a chunk's last tile, the causal
@@ -179,10 +204,10 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
     float smax = -INFINITY;
     if (edge) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kt + 16 * ks + 4 * q4 + i;
+          const int key = kt + 16 * (ks0 + ks) + 4 * q4 + i;
           bool vis = key < k1;
           if (TREE)
             vis = vis && (key < tail0 || ((anc >> ((unsigned)(key - tail0) & 31u)) & 1u));
@@ -193,7 +218,7 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
         }
     } else {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
         for (int i = 0; i < 4; ++i) smax = fmaxf(smax, s[ks][i]);
     }
@@ -204,7 +229,7 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
     m = mn;
     float ps = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = exp2_raw(__builtin_fmaf(s[ks][i], a.scale_log2, -mn));
@@ -215,9 +240,9 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
     // P as a bf16 pair hi + lo (hi = bf16(p), lo = bf16(p - hi)): the P.V product keeps ~16
     // significant bits of p, so the bf16 output rounding is the only error of note (a single
     // bf16 P, as the reference's kernel rounds it, leaves little margin on long flat rows).
-    u32x4_t ph[2], pl[2];
+    u32x4_t ph[NU], pl[NU];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -227,23 +252,76 @@ __global__ __launch_bounds__(64 * WV) void attn_p1_kernel(const AttnArgs a) {
           ph[u][2 * h + i] = hi;
           pl[u][2 * h + i] = pack_bf16x2(a0 - bf2f(hi & 0xFFFFu), a1 - bf2f(hi >> 16));
         }
+    // the running max rarely moves after the first tiles: rescale only when some row's did
+    // (alpha == 1 exactly otherwise, so skipping the multiply changes no bit)
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) o[t] *= alpha;
+    }
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      o[t] *= alpha;
       const int d = 16 * t + c16;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(&vt_lds[vt_off(d, 32 * u + 8 * q4)]);
+      for (int u = 0; u < NU; ++u) {
+        const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(&vt_lds[vt_off(d, 32 * (kh * NU + u) + 8 * q4)]);
         o[t] = mfma16x16x32(vf, ph[u], o[t]);
         o[t] = mfma16x16x32(vf, pl[u], o[t]);
       }
     }
-  }
-  if (!active) return;
+  };
 
+  // PF tiles in flight: tile kt is staged from the registers its load landed in, which then
+  // take the load of tile kt + PF*KT while tile kt is computed.
+  TileRegs r0, r1;
+  auto step = [&](TileRegs& r, int kt) {
+    __syncthreads();  // previous tile fully consumed
+    store_tile(r);
+    __syncthreads();
+    if (kt + PF * KT < k1) load_tile(r, kt + PF * KT);
+    if (active) compute_tile(kt);
+  };
+  if (k0 < k1) load_tile(r0, k0);
+  if constexpr (PF == 1) {
+    for (int kt = k0; kt < k1; kt += KT) step(r0, kt);
+  } else {
+    if (k0 + KT < k1) load_tile(r1, k0 + KT);
+    for (int kt = k0; kt < k1; kt += 2 * KT) {
+      step(r0, kt);
+      if (kt + KT < k1) step(r1, kt + KT);
+    }
+  }
   // ---- finalize: lane (row c16, quarter q4) holds O^T[16t + 4q4 + i][row]
   l += shfl_xor(l, 16);
   l += shfl_xor(l, 32);
+  if constexpr (KS == 2) {
+    // key half 1 hands (m, l, O) to half 0 through LDS: M = max(m0, m1),
+    // O = 2^(m0 - M) O0 + 2^(m1 - M) O1, l likewise
+    float* mo = reinterpret_cast<float*>(smem);           // [WV][NDT][64 lanes][4]
+    float* ml = mo + WV * NDT * 64 * 4;                   // [WV][16] m, then [WV][16] l
+    __syncthreads();                                      // every wave is done with the last tile
+    if (kh == 1 && active) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) *reinterpret_cast<f32x4_t*>(&mo[((rtw * NDT + t) * 64 + lane) * 4]) = o[t];
+      if (q4 == 0) {
+        ml[rtw * 16 + c16] = m;
+        ml[WV * 16 + rtw * 16 + c16] = l;
+      }
+    }
+    __syncthreads();
+    if (kh == 1 || !active) return;
+    const float m1 = ml[rtw * 16 + c16], l1 = ml[WV * 16 + rtw * 16 + c16];
+    const float mm = fmaxf(m, m1);
+    const float a0 = exp2_raw(m - mm), a1 = exp2_raw(m1 - mm);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const f32x4_t o1 = *reinterpret_cast<const f32x4_t*>(&mo[((rtw * NDT + t) * 64 + lane) * 4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[t][i] = __builtin_fmaf(o[t][i], a0, o1[i] * a1);
+    }
+    l = __builtin_fmaf(l, a0, l1 * a1);
+    m = mm;
+  }
+  if (!active) return;
   const int row = rt * 16 + c16;
   if (row >= a.R) return;
   if (a.NB == 1) {
@@ -339,7 +417,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
 }
 
 struct Plan {
-  int R, RT, RP, WV, NRG, chunk, NB;
+  int R, RT, RP, WV, KS, PF, NRG, chunk, NB;
 };
 
 Plan make_plan(long B, long Hq, long Hk, long Mq, long L) {
@@ -348,16 +426,21 @@ Plan make_plan(long B, long Hq, long Hk, long Mq, long L) {
   p.RT = (p.R + 15) / 16;
   p.RP = p.RT * 16;
   p.WV = p.RT > 4 ? 8 : 4;
+  p.KS = 1;
+  p.PF = p.WV == 8 ? 2 : 1;
   p.NRG = (p.RT + p.WV - 1) / p.WV;
-  // ~2 workgroups per CU (256 CUs) on long caches; at least 4 tiles (256 keys) per block so
-  // the fp32 partials stay a small fraction of the KV stream. Row groups beyond one re-read
-  // the head's K/V (only when gqa * Mq > 128).
+  // Long caches: ~2 workgroups of 4 waves per CU (256 CUs), or one of 8 waves (twice the
+  // rows per K/V tile: the fp32 partials, written here and read by the combine, double too),
+  // which then keeps two tiles in flight. At least 4 tiles (256 keys) per block. When that
+  // caps the blocks below one workgroup per CU, 4-row-tile heads split each tile's keys over
+  // 8 waves. Row groups beyond one re-read the head's K/V (only when gqa * Mq > 128).
   const long heads = B * Hk * p.NRG;
-  const long target = 512;
+  const long target = p.WV == 8 ? 256 : 512;
   long nb = (target + heads - 1) / heads;
   const long max_nb = (L + 4 * KT - 1) / (4 * KT);
   if (nb > max_nb) nb = max_nb;
   if (nb < 1) nb = 1;
+  if (p.WV == 4 && heads * nb < 256) p.KS = 2;
   long chunk = (L + nb - 1) / nb;
   chunk = ((chunk + KT - 1) / KT) * KT;
   p.chunk = (int)chunk;
@@ -432,6 +515,10 @@ int verify_attention_impl(const void* q, int64_t B, int64_t Hq, int64_t Mq, int6
   for (int i = 0; i < 3; ++i)
     if ((k_strides[i] % 8) || (v_strides[i] % 8) || k_strides[i] < 0 || v_strides[i] < 0)
       return fail(DSPARK_ERR_ALIGN, "verify_attention: K/V strides must be non-negative multiples of 8 elements");
+  // the kernels address a 64-key tile with 32-bit byte offsets from its first key
+  if (k_strides[2] >= (1L << 24) || v_strides[2] >= (1L << 24))
+    return fail(DSPARK_ERR_SHAPE, "verify_attention: K/V position stride %ld/%ld too large", (long)k_strides[2],
+                (long)v_strides[2]);
   const Plan p = make_plan(B, Hq, Hk, Mq, L_total);
   const size_t need = workspace_bytes(p, B, Hk, D);
   if (need && (!workspace || workspace_bytes_ < need))
@@ -474,9 +561,10 @@ int verify_attention_impl(const void* q, int64_t B, int64_t Hq, int64_t Mq, int6
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid1((unsigned)(B * Hk), (unsigned)p.NB, (unsigned)p.NRG);
   const bool tree = tree_anc != nullptr;
-#define ATTN_P1(DD, TR, W) hipLaunchKernelGGL((attn_p1_kernel<DD, TR, W>), grid1, dim3(64 * W), 0, s, a)
+#define ATTN_P1(DD, TR, W, K, F) \
+  hipLaunchKernelGGL((attn_p1_kernel<DD, TR, W, K, F>), grid1, dim3(64 * W * K), 0, s, a)
 #define ATTN_P1_W(DD, TR) \
-  if (p.WV == 8) ATTN_P1(DD, TR, 8); else ATTN_P1(DD, TR, 4);
+  if (p.WV == 8) ATTN_P1(DD, TR, 8, 1, 2); else if (p.KS == 2) ATTN_P1(DD, TR, 4, 2, 1); else ATTN_P1(DD, TR, 4, 1, 1);
   if (D == 128) {
     if (tree) { ATTN_P1_W(128, true) } else { ATTN_P1_W(128, false) }
   } else {
