@@ -33,7 +33,7 @@ namespace {
 
 constexpr int kNS = 4;             // waves (16-row output tiles) per workgroup: 64-row strips
 constexpr int kStripRows = 16 * kNS;
-constexpr int kTargetWorkgroups = 512;  // two per CU on 256 CUs
+constexpr long kCUs = 256;         // MI355X
 // Split-K arrival counters live in a fixed region at the start of the workspace, the same bytes
 // for every shape, so partials of one shape never land on another shape's counters (each
 // launch leaves its counters at zero).
@@ -58,9 +58,17 @@ Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
   for (int i = 0; i < count; ++i) strips += (Ns[i] + kStripRows - 1) / kStripRows;
   p.strips = (int)strips;
   p.mtiles = (int)((M + 15) / 16);
-  // 16 groups (1024 k) per slice; 8 when that leaves fewer than kTargetWorkgroups workgroups
+  // 16 groups (1024 k) per slice, unless those workgroups fill their last resident round
+  // (one or two rounds) poorly and 8-group slices, whose kernels keep more workgroups per CU,
+  // fill theirs better. Resident workgroups per CU of the instantiations (VGPR-limited, as
+  // compiled): 16-group 3 (8-bit) / 4 (4-bit), 8-group 5.
   long s = (G + 15) / 16;
-  if (strips * s < kTargetWorkgroups) s = (G + 7) / 8;
+  {
+    auto fill = [&](long w, long slots) { return (double)w / (double)(((w + slots - 1) / slots) * slots); };
+    const long slots16 = kCUs * (bits == 8 ? 3 : 4), slots8 = kCUs * 5;
+    const long w16 = strips * s, s8 = (G + 7) / 8;
+    if (w16 <= 2 * slots16 && fill(w16, slots16) < 0.9 && fill(strips * s8, slots8) > fill(w16, slots16)) s = s8;
+  }
   if (s > kQmmMaxSlices) s = kQmmMaxSlices;
   if (s < 1) s = 1;
   p.S = (int)s;
