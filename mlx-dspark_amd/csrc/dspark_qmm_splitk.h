@@ -20,6 +20,10 @@ namespace dspark {
 constexpr int kQmmMaxProblems = DSPARK_QMM_MAX_PROBLEMS;
 constexpr int kQmmMaxSlices = 32;
 constexpr int kSliceChunk = 8;  // partials the last arriver requests at a time
+// buffer resource word 3 for gfx9-family raw buffers, and the sc1 (device-coherent) cache
+// policy of buffer loads and stores
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kCoherentSc1 = 16;
 
 struct QmmSkProb {
   const u16* x;
@@ -27,7 +31,7 @@ struct QmmSkProb {
   const u16* s;
   const u16* b;
   u16* y;
-  float* part;  // [mtiles][strips][S][16][16*NS] fp32 partials (S > 1)
+  float* part;  // [mtiles][strips][S][16*NS columns][16 rows] fp32 partials (S > 1)
   int* ctr;     // [mtiles][strips] arrival counters (zero between calls)
   long ldx;
   long ldy;
@@ -355,46 +359,42 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   // Partials travel through device-coherent (sc1) stores and loads, so no L2 write-back or
   // invalidate is needed: each thread waits for its stores to complete before the workgroup
   // arrives on the strip's counter (device-scope atomic), and the last arriver reads the other
-  // slices with coherent loads, summing in slice order.
+  // slices with coherent loads, summing in slice order. A strip's partials are
+  // [S][TW columns][16 rows] fp32: a lane's 4 rows of one column are one 16-byte chunk, so each
+  // wave stores 1 KB contiguous and the last arriver reads one chunk per slice per thread.
   constexpr int TW = 16 * NS;  // strip width
   const long tile = (long)mt * P.strips + strip;
-  float* part = P.part + (tile * S) * (16 * TW);
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    __hip_atomic_store(&part[(long)sl * (16 * TW) + (4 * q + r) * TW + 16 * wave + c16], acc[r], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(P.part + (tile * S) * (16 * TW), 0, S * 16 * TW * 4, kBufferRsrcWord3);
+  const f32x4_t accv = acc;
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, accv), prs,
+                                         ((sl * TW + 16 * wave + c16) * 16 + 4 * q) * 4, 0, kCoherentSc1);
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this thread's partial stores are complete
   __syncthreads();
   if (tid == 0)
     last_flag = (__hip_atomic_fetch_add(&P.ctr[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1);
   __syncthreads();
   if (!last_flag) return;
-  // 16*TW outputs, 4 per thread; all S partials of all 4 are requested before summing
-  // 16*TW outputs, 4 per thread, summed in slice order; kSliceChunk slices are requested
-  // at a time for all 4
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  // thread -> (column tid / 4, rows 4 (tid % 4) .. + 3): one chunk per slice, summed in slice
+  // order; kSliceChunk slices are requested at a time
+  static_assert(TW * 4 == 64 * NS, "one 4-row chunk per thread");
+  const int col = tid >> 2, rq = tid & 3;
+  f32x4_t v = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < S; s0 += kSliceChunk) {
-    float pv[4][kSliceChunk];
+    u32x4_t pv[kSliceChunk];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + i * 64 * NS;
+    for (int s2 = 0; s2 < kSliceChunk; ++s2)
+      pv[s2] = __builtin_amdgcn_raw_buffer_load_b128(prs, ((min(s0 + s2, S - 1) * TW + col) * 16 + 4 * rq) * 4, 0,
+                                                     kCoherentSc1);
 #pragma unroll
-      for (int s2 = 0; s2 < kSliceChunk; ++s2)
-        pv[i][s2] = __hip_atomic_load(&part[(long)min(s0 + s2, S - 1) * (16 * TW) + e], __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int s2 = 0; s2 < kSliceChunk; ++s2)
-        if (s0 + s2 < S) v[i] += pv[i][s2];
+    for (int s2 = 0; s2 < kSliceChunk; ++s2)
+      if (s0 + s2 < S) v += __builtin_bit_cast(f32x4_t, pv[s2]);
   }
+  const int nc = strip * TW + col;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid + i * 64 * NS;
-    const int m = e / TW, col = e - m * TW;
-    const int nc = strip * TW + col;
-    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v[i]);
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * rq + r;
+    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v[r]);
   }
   if (tid == 0) __hip_atomic_store(&P.ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
