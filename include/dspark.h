@@ -149,6 +149,30 @@ int dspark_qmm_packed_multi(const dspark_qmm_packed_problem* problems, int count
 size_t dspark_qmm_packed_multi_workspace(const dspark_qmm_packed_problem* problems, int count, int64_t M,
                                          int bits, int group_size);
 
+/*
+ * Fused gate / up / SwiGLU for the MLP of a verify forward (no counterpart in the reference,
+ * which runs the two quantized matmuls and silu(gate) * up as three ops (target.py:187-221 ->
+ * mlx-lm's MLP); this replaces that sequence for packed weights):
+ *   h[m, n] = bf16( bf16(g * bf16(sigmoid(g))) * u ),  g = bf16(x W_gate^T)[m, n],
+ *                                                     u = bf16(x W_up^T)[m, n]
+ * bit for bit what dspark_qmm_packed_multi over the two matrices followed by dspark_swiglu
+ * gives when N is a multiple of 64 (same K slices; otherwise within the qmm tolerance).
+ * dspark_qmm_pack_swiglu writes the pair form: the packed layout of 2 * ceil(N / 16) row
+ * tiles, gate tile t then up tile t (K % 512 == 0); dspark_qmm_swiglu_packed_bytes sizes it.
+ * x bf16 [M, K] (ldx), h bf16 [M, N] (ldh); workspace as for dspark_qmm_packed_multi.
+ */
+size_t dspark_qmm_swiglu_packed_bytes(int64_t N, int64_t K, int bits, int group_size);
+
+int dspark_qmm_pack_swiglu(const uint32_t* gate_w, const void* gate_scales, const void* gate_biases,
+                           const uint32_t* up_w, const void* up_scales, const void* up_biases, int64_t N, int64_t K,
+                           int bits, int group_size, void* packed, size_t packed_bytes, dspark_stream stream);
+
+int dspark_qmm_swiglu_packed(const void* x, int64_t ldx, const void* packed, void* h, int64_t ldh, int64_t N,
+                             int64_t K, int64_t M, int bits, int group_size, void* workspace,
+                             size_t workspace_bytes, dspark_stream stream);
+
+size_t dspark_qmm_swiglu_packed_workspace(int64_t N, int64_t K, int64_t M, int bits, int group_size);
+
 /* ------------------------------------------------------------------ verify attention */
 
 /*

@@ -27,6 +27,13 @@ __device__ __forceinline__ u16 f2bf(float f) {
   return __builtin_bit_cast(u16, (__bf16)f);
 }
 
+// SwiGLU of bf16 gate and up values as mlx rounds it: bf16(bf16(g * bf16(sigmoid(g))) * u)
+// (the caller rounds the returned product)
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+  const float sg = bf2f(f2bf(1.0f / (1.0f + expf(-g))));
+  return bf2f(f2bf(g * sg)) * u;
+}
+
 __device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
   bf16x2_t p = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(u32, p);

@@ -89,11 +89,11 @@ Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
   return p;
 }
 
-template <int BITS, int KSMAX, bool SBVEC, bool PACKED = false>
+template <int BITS, int KSMAX, bool SBVEC, bool PACKED = false, bool SWIGLU = false>
 int launch(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
-  hipLaunchKernelGGL((qmm_sk_kernel<BITS, kNS, KSMAX, SBVEC, PACKED>), dim3(p.strips, p.S, p.mtiles), dim3(64 * kNS), 0,
-                     st, a);
-  return check_launch(PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
+  hipLaunchKernelGGL((qmm_sk_kernel<BITS, kNS, KSMAX, SBVEC, PACKED, SWIGLU>), dim3(p.strips, p.S, p.mtiles),
+                     dim3(64 * kNS), 0, st, a);
+  return check_launch(SWIGLU ? "dspark_qmm_swiglu_packed" : PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
 }
 
 template <int BITS>
@@ -102,10 +102,10 @@ int launch_bits(const QmmSkArgs& a, const Plan& p, bool sbvec, hipStream_t st) {
   return sbvec ? launch<BITS, 16, true>(a, p, st) : launch<BITS, 16, false>(a, p, st);
 }
 
-template <int BITS>
+template <int BITS, bool SWIGLU = false>
 int launch_packed(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
-  if (p.ksmax == 8) return launch<BITS, 8, true, true>(a, p, st);
-  return launch<BITS, 16, true, true>(a, p, st);
+  if (p.ksmax == 8) return launch<BITS, 8, true, true, SWIGLU>(a, p, st);
+  return launch<BITS, 16, true, true, SWIGLU>(a, p, st);
 }
 
 // ---- the packed form (dspark_qmm_pack). Per matrix, T = ceil(N/16) row tiles, G = K/64:
@@ -115,7 +115,8 @@ int launch_packed(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
 //                  4-bit: bytes [8qs, 8qs+8) of group 2j then of group 2j+1, qs = 2(q&1) + (q>>1)
 //                  (the lane order the MFMA loop uses; see WSlice);
 //   scale/bias   T x G/8 octets x {scales, biases} x 16 rows x 8 bf16.
-// Rows >= N are zero.
+// Rows >= N are zero. The SwiGLU pair form (dspark_qmm_pack_swiglu) is this layout for 2T tiles,
+// tile 2t = gate tile t, tile 2t + 1 = up tile t.
 struct PackedLayout {
   long tiles, wchunks, schunks;
   size_t bytes() const { return (size_t)(wchunks + schunks) * 16; }
@@ -129,16 +130,23 @@ PackedLayout packed_layout(long N, long K, int bits) {
   return L;
 }
 
-__global__ __launch_bounds__(256) void pack_kernel(const unsigned char* __restrict__ w, const u16* __restrict__ s,
-                                                   const u16* __restrict__ b, long N, int K, int bits, long wchunks,
-                                                   long schunks, unsigned char* __restrict__ out) {
+// pair (w2 != null): destination tile t takes tile t / 2 of the first matrix (t even) or of
+// the second (t odd)
+__global__ __launch_bounds__(256) void pack_kernel(const unsigned char* __restrict__ w1, const u16* __restrict__ s1,
+                                                   const u16* __restrict__ b1, const unsigned char* __restrict__ w2,
+                                                   const u16* __restrict__ s2, const u16* __restrict__ b2, long N,
+                                                   int K, int bits, long wchunks, long schunks,
+                                                   unsigned char* __restrict__ out) {
   const long c = (long)blockIdx.x * 256 + threadIdx.x;
   const int G = K >> 6;
+  const bool pair = w2 != nullptr;
   u32x4_t v = {0u, 0u, 0u, 0u};
   if (c < wchunks) {
     const int per_tile = bits == 4 ? (G >> 1) : G;
-    const long t = c / (per_tile * 64);
-    const int rem = (int)(c - t * per_tile * 64), j = rem >> 6, l = rem & 63;
+    const long tt = c / (per_tile * 64);
+    const int rem = (int)(c - tt * per_tile * 64), j = rem >> 6, l = rem & 63;
+    const long t = pair ? tt >> 1 : tt;
+    const unsigned char* w = (pair && (tt & 1)) ? w2 : w1;
     const long r = 16 * t + (l & 15);
     const int q = l >> 4;
     if (r < N) {
@@ -155,10 +163,12 @@ __global__ __launch_bounds__(256) void pack_kernel(const unsigned char* __restri
     const long c2 = c - wchunks;
     const long blk = c2 >> 5;
     const int rem = (int)(c2 & 31), arr = rem >> 4, r16 = rem & 15;
-    const long t = blk / (G >> 3);
-    const int o = (int)(blk - t * (G >> 3));
+    const long tt = blk / (G >> 3);
+    const int o = (int)(blk - tt * (G >> 3));
+    const long t = pair ? tt >> 1 : tt;
+    const bool second = pair && (tt & 1);
     const long r = 16 * t + r16;
-    if (r < N) v = ldg128((arr ? b : s) + r * G + 8 * o);
+    if (r < N) v = ldg128((arr ? (second ? b2 : b1) : (second ? s2 : s1)) + r * G + 8 * o);
   } else {
     return;
   }
@@ -364,9 +374,100 @@ extern "C" int dspark_qmm_pack(const uint32_t* w, const void* scales, const void
   const long chunks = L.wchunks + L.schunks;
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), reinterpret_cast<const unsigned char*>(w),
-                     static_cast<const u16*>(scales), static_cast<const u16*>(biases), (long)N, (int)K, bits,
-                     L.wchunks, L.schunks, static_cast<unsigned char*>(packed));
+                     static_cast<const u16*>(scales), static_cast<const u16*>(biases), nullptr, nullptr, nullptr,
+                     (long)N, (int)K, bits, L.wchunks, L.schunks, static_cast<unsigned char*>(packed));
   return check_launch("dspark_qmm_pack");
+}
+
+// ---- fused gate / up / SwiGLU over the pair form: rows of the pair buffer = 32 ceil(N / 16)
+namespace {
+long swiglu_rows(int64_t N) { return 32 * ((N + 15) / 16); }
+}  // namespace
+
+extern "C" size_t dspark_qmm_swiglu_packed_bytes(int64_t N, int64_t K, int bits, int group_size) {
+  if (check_common(1, K, N, bits, group_size) || K % 512) return 0;
+  return packed_layout(swiglu_rows(N), K, bits).bytes();
+}
+
+extern "C" int dspark_qmm_pack_swiglu(const uint32_t* gate_w, const void* gate_scales, const void* gate_biases,
+                                      const uint32_t* up_w, const void* up_scales, const void* up_biases, int64_t N,
+                                      int64_t K, int bits, int group_size, void* packed, size_t packed_bytes,
+                                      dspark_stream stream) {
+  int st = check_common(1, K, N, bits, group_size);
+  if (st) return st;
+  if (K % 512) return fail(DSPARK_ERR_SHAPE, "qmm_pack_swiglu: K=%lld is not a multiple of 512", (long long)K);
+  if (!gate_w || !gate_scales || !gate_biases || !up_w || !up_scales || !up_biases || !packed)
+    return fail(DSPARK_ERR_ARG, "qmm_pack_swiglu: null pointer");
+  if (!aligned(gate_w, 16) || !aligned(gate_scales, 16) || !aligned(gate_biases, 16) || !aligned(up_w, 16) ||
+      !aligned(up_scales, 16) || !aligned(up_biases, 16) || !aligned(packed, 16))
+    return fail(DSPARK_ERR_ALIGN, "qmm_pack_swiglu: every buffer must be 16-byte aligned");
+  const PackedLayout L = packed_layout(swiglu_rows(N), K, bits);
+  if (packed_bytes < L.bytes())
+    return fail(DSPARK_ERR_WORKSPACE, "qmm_pack_swiglu: packed buffer %zu < %zu bytes", packed_bytes, L.bytes());
+  const long chunks = L.wchunks + L.schunks;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), reinterpret_cast<const unsigned char*>(gate_w),
+                     static_cast<const u16*>(gate_scales), static_cast<const u16*>(gate_biases),
+                     reinterpret_cast<const unsigned char*>(up_w), static_cast<const u16*>(up_scales),
+                     static_cast<const u16*>(up_biases), (long)N, (int)K, bits, L.wchunks, L.schunks,
+                     static_cast<unsigned char*>(packed));
+  return check_launch("dspark_qmm_pack_swiglu");
+}
+
+extern "C" size_t dspark_qmm_swiglu_packed_workspace(int64_t N, int64_t K, int64_t M, int bits, int group_size) {
+  if (check_common(M, K, N, bits, group_size) || K % 512) return 0;
+  long Ns[1] = {swiglu_rows(N)};
+  const Plan p = make_plan(Ns, 1, K, M, bits);
+  return p.ctr_bytes + p.part_bytes;
+}
+
+extern "C" int dspark_qmm_swiglu_packed(const void* x, int64_t ldx, const void* packed, void* h, int64_t ldh,
+                                        int64_t N, int64_t K, int64_t M, int bits, int group_size, void* workspace,
+                                        size_t workspace_bytes, dspark_stream stream) {
+  int st = check_common(M, K, N, bits, group_size);
+  if (st) return st;
+  if (K % 512) return fail(DSPARK_ERR_SHAPE, "qmm_swiglu_packed: K=%lld is not a multiple of 512", (long long)K);
+  if (!x || !packed || !h) return fail(DSPARK_ERR_ARG, "qmm_swiglu_packed: null pointer");
+  if (!aligned(x, 16) || ldx % 8 || !aligned(packed, 16) || !aligned(h, 2))
+    return fail(DSPARK_ERR_ALIGN, "qmm_swiglu_packed: x 16-byte aligned with ldx %% 8 == 0, packed 16-byte aligned");
+  if (ldx < K || ldh < N)
+    return fail(DSPARK_ERR_SHAPE, "qmm_swiglu_packed: ldx=%lld < K or ldh=%lld < N", (long long)ldx, (long long)ldh);
+  long Ns[1] = {swiglu_rows(N)};
+  const Plan p = make_plan(Ns, 1, K, M, bits);
+  if (p.S == 0) return fail(DSPARK_ERR_SHAPE, "qmm_swiglu_packed: M=%lld needs too many split-K counters", (long long)M);
+  const size_t need = p.ctr_bytes + p.part_bytes;
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(DSPARK_ERR_WORKSPACE, "qmm_swiglu_packed: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (need && !aligned(workspace, 256))
+    return fail(DSPARK_ERR_ALIGN, "qmm_swiglu_packed: workspace must be 256-byte aligned");
+  const PackedLayout L = packed_layout(Ns[0], K, bits);
+  QmmSkArgs a{};
+  a.count = 1;
+  a.M = (int)M;
+  a.S = p.S;
+  QmmSkProb& d = a.p[0];
+  d.x = static_cast<const u16*>(x);
+  d.w = static_cast<const u32*>(packed);
+  d.s = reinterpret_cast<const u16*>(static_cast<const char*>(packed) + (size_t)L.wchunks * 16);
+  d.b = d.s;
+  d.y = static_cast<u16*>(h);
+  d.ldx = ldx;
+  d.ldy = ldh;
+  d.N = (int)Ns[0];
+  d.hN = (int)N;
+  d.K = (int)K;
+  d.strips = p.strips;
+  d.strip0 = 0;
+  if (need) {
+    d.ctr = static_cast<int*>(workspace);
+    d.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.ctr_bytes);
+  }
+  for (int i = 1; i < kQmmMaxProblems; ++i) {
+    a.p[i] = a.p[0];
+    a.p[i].strip0 = 1 << 30;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return bits == 4 ? launch_packed<4, true>(a, p, s) : launch_packed<8, true>(a, p, s);
 }
 
 extern "C" int dspark_qmm_packed_multi(const dspark_qmm_packed_problem* problems, int count, int64_t M, int bits,

@@ -39,6 +39,7 @@ struct QmmSkProb {
   int K;
   int strip0;  // first blockIdx.x of this problem
   int strips;
+  int hN;      // SWIGLU: width of y (= h), the unpadded gate / up rows
 };
 
 struct QmmSkArgs {
@@ -162,14 +163,21 @@ __device__ __forceinline__ void group_fma(u32x4_t a0, u32x4_t a1, f32x4_t c, u32
 // PACKED: the weights and scales/biases come in the tiled form dspark_qmm_pack writes (see
 // pack_* below): P.w is the tile stream, P.s the scale/bias tiles (P.b unused); requires
 // SBVEC (G % 8 == 0). Same products, bit for bit, as the reference layout.
-template <int BITS, int NS, int KSMAX, bool SBVEC, bool PACKED = false>
+// SWIGLU (packed only): the tiles alternate gate tile t, up tile t (dspark_qmm_pack_swiglu),
+// so a strip holds 2 gate and 2 up tiles and its finished sums become
+// h = bf16(swiglu(bf16(gate), bf16(up))) for 32 columns of h, the same values an unfused
+// gate / up launch and the SwiGLU kernel produce.
+template <int BITS, int NS, int KSMAX, bool SBVEC, bool PACKED = false, bool SWIGLU = false>
 __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   static_assert(!PACKED || SBVEC, "the packed form needs 8-group slices");
+  static_assert(!SWIGLU || PACKED, "the fused SwiGLU reads the interleaved packed form");
   constexpr int XP = KSMAX * 64 + 8;  // LDS row pitch of the staged x slice (elements)
   __shared__ __attribute__((aligned(16))) u16 xs[16 * XP];
   // per group: 16 row sums (8-bit: sum x; 4-bit: -128 * sum x, the MFMA seed)
   __shared__ __attribute__((aligned(16))) float xsum[KSMAX * 16];
   __shared__ int last_flag;
+  // SWIGLU: the strip's finished sums, [16*NS columns][16 rows] (pitch 17)
+  __shared__ float hsum[SWIGLU ? 16 * NS * 17 : 1];
   // SBVEC: scales (0) and biases (1) of the strip's 16*NS rows over the slice, row pitch
   // SBP (16-byte rows; 4-byte reads of 16 consecutive rows fall in distinct banks)
   constexpr int SBP = KSMAX + 8;
@@ -348,7 +356,28 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   }
 
   // ---- 6. epilogue: lane holds y[m_base + 4q + r][ncol]
+  constexpr int TW = 16 * NS;  // strip width
+  // SWIGLU: thread -> h columns 32 * strip + (tid >> 3) of rows 2 (tid & 7), +1; gate tile 2s + j
+  // of the strip is its columns 32 j .. 32 j + 15, the matching up tile the next 16
+  auto swiglu_out = [&]() {
+    const int hc = tid >> 3, r0 = 2 * (tid & 7);
+    const int gc = 32 * (hc >> 4) + (hc & 15);
+    const int col = strip * (TW / 2) + hc;
+#pragma unroll
+    for (int r = r0; r < r0 + 2; ++r) {
+      const float g = bf2f(f2bf(hsum[gc * 17 + r])), u = bf2f(f2bf(hsum[(gc + 16) * 17 + r]));
+      if (r < m_rows && col < P.hN) P.y[(long)(m_base + r) * P.ldy + col] = f2bf(swiglu_bf16(g, u));
+    }
+  };
+  static_assert(!SWIGLU || TW * 8 == 2 * 64 * NS, "two SwiGLU outputs per thread");
   if (S == 1) {
+    if constexpr (SWIGLU) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hsum[(16 * wave + c16) * 17 + 4 * q + r] = acc[r];
+      __syncthreads();
+      swiglu_out();
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 4 * q + r;
@@ -362,7 +391,6 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
   // slices with coherent loads, summing in slice order. A strip's partials are
   // [S][TW columns][16 rows] fp32: a lane's 4 rows of one column are one 16-byte chunk, so each
   // wave stores 1 KB contiguous and the last arriver reads one chunk per slice per thread.
-  constexpr int TW = 16 * NS;  // strip width
   const long tile = (long)mt * P.strips + strip;
   const __amdgpu_buffer_rsrc_t prs =
       __builtin_amdgcn_make_buffer_rsrc(P.part + (tile * S) * (16 * TW), 0, S * 16 * TW * 4, kBufferRsrcWord3);
@@ -390,11 +418,18 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     for (int s2 = 0; s2 < kSliceChunk; ++s2)
       if (s0 + s2 < S) v += __builtin_bit_cast(f32x4_t, pv[s2]);
   }
-  const int nc = strip * TW + col;
+  if constexpr (SWIGLU) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * rq + r;
-    if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v[r]);
+    for (int r = 0; r < 4; ++r) hsum[col * 17 + 4 * rq + r] = v[r];
+    __syncthreads();
+    swiglu_out();
+  } else {
+    const int nc = strip * TW + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * rq + r;
+      if (m < m_rows && nc < N) P.y[(long)(m_base + m) * P.ldy + nc] = f2bf(v[r]);
+    }
   }
   if (tid == 0) __hip_atomic_store(&P.ctr[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

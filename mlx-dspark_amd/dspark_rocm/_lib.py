@@ -97,6 +97,12 @@ SIGNATURES: dict[str, tuple] = {
                                         c_size_t, c_void_p]),
     "dspark_qmm_packed_multi_workspace": (c_size_t, [ctypes.POINTER(QmmPackedProblem), c_int, c_i64, c_int,
                                                      c_int]),
+    "dspark_qmm_swiglu_packed_bytes": (c_size_t, [c_i64, c_i64, c_int, c_int]),
+    "dspark_qmm_pack_swiglu": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_i64,
+                                       c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "dspark_qmm_swiglu_packed": (c_int, [c_void_p, c_i64, c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64, c_int,
+                                         c_int, c_void_p, c_size_t, c_void_p]),
+    "dspark_qmm_swiglu_packed_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_int, c_int]),
     "dspark_verify_attention": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_i64_p,
                                         c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                         c_size_t, c_void_p]),

@@ -14,9 +14,10 @@ Two forwards of the same weights live here:
   mlx-lm. Norms and RoPE are torch ops with the same bf16 rounding points as the kernels.
 * :class:`VerifyEngine` — the MI355X verify step: per layer one fused residual-add + RMSNorm,
   one q/k/v qmm launch, one q/k-norm + RoPE + cache-write kernel, split-KV attention writing
-  o_proj's input rows directly, the o qmm, residual-add + RMSNorm, one gate/up qmm launch,
-  SwiGLU, the down qmm; then the final norm, lm_head, device argmax and greedy accept. All
-  buffers are preallocated, so a step can be captured in a hipGraph.
+  o_proj's input rows directly, the o qmm, residual-add + RMSNorm, one fused gate/up/SwiGLU
+  qmm launch (packed weights; else a gate/up launch and the SwiGLU kernel), the down qmm; then
+  the final norm, lm_head, device argmax and greedy accept. All buffers are preallocated, so a
+  step can be captured in a hipGraph.
 
 :class:`Target` mirrors the reference's ``verify`` / ``rollback`` / ``make_cache`` surface and
 the greedy round (generate.py:1544-1593).
@@ -167,17 +168,27 @@ class VerifyEngine:
     """Preallocated fused verify step for up to ``max_rows`` rows (batch 1). With ``packed``,
     every projection whose K is a multiple of 512 is held (also) in the MI355X packed qmm form
     (``ops.qmm_pack``, packed once here) and multiplied from it; products are bit-identical to
-    the reference layout's."""
+    the reference layout's. Each MLP's gate and up projections are packed as one pair
+    (``ops.qmm_pack_swiglu``) and run as one fused gate / up / SwiGLU launch, bit-identical to
+    the two products followed by SwiGLU when the intermediate size is a multiple of 64."""
 
     def __init__(self, model: DenseModel, max_rows: int = 16, packed: bool = True):
         a = model.args
         self.model, self.args, self.max_rows = model, a, max_rows
         self._packed: dict[int, ops.PackedQmm] = {}
+        self._swiglu: dict[int, ops.PackedSwiGLU] = {}
         if packed:
             mods = [model.lm_head]
             for layer in model.layers:
                 at, mlp = layer.self_attn, layer.mlp
-                mods += [at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj]
+                mods += [at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.down_proj]
+                g, u = mlp.gate_proj, mlp.up_proj
+                n, k = g.weight.shape[0], g.weight.shape[1] * 32 // g.bits
+                if g.bits == u.bits and g.weight.shape == u.weight.shape and ops.qmm_packable(n, k, g.bits):
+                    self._swiglu[id(mlp)] = ops.qmm_pack_swiglu((g.weight, g.scales, g.biases),
+                                                                (u.weight, u.scales, u.biases), bits=g.bits)
+                else:
+                    mods += [g, u]
             for mod in mods:
                 n, k = mod.weight.shape[0], mod.weight.shape[1] * 32 // mod.bits
                 if ops.qmm_packable(n, k, mod.bits):
@@ -235,8 +246,12 @@ class VerifyEngine:
             ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1)
             self._qmm(att, [at.o_proj], [r])
             ops.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
-            self._qmm(y, [mlp.gate_proj, mlp.up_proj], [self.g[:M], self.u[:M]])
-            ops.swiglu(self.g[:M], self.u[:M], out=self.hm[:M])
+            pair = self._swiglu.get(id(mlp))
+            if pair is not None:
+                ops.quantized_swiglu_packed(y, pair, out=self.hm[:M])
+            else:
+                self._qmm(y, [mlp.gate_proj, mlp.up_proj], [self.g[:M], self.u[:M]])
+                ops.swiglu(self.g[:M], self.u[:M], out=self.hm[:M])
             self._qmm(self.hm[:M], [mlp.down_proj], [r])
         ops.rmsnorm(h, m.norm, eps, residual=r, h_out=h, out=y)
         lm = m.lm_head

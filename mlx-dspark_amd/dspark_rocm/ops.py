@@ -206,6 +206,57 @@ def quantized_matmul_packed(x: torch.Tensor, packed: PackedQmm, *, out: torch.Te
     return quantized_matmul_packed_multi([x], [packed], outs=None if out is None else [out])[0]
 
 
+class PackedSwiGLU:
+    """Gate and up [N, K] matrices in the pair form (``dspark_qmm_pack_swiglu``): the packed
+    layout of 2 ceil(N/16) row tiles, gate tile t then up tile t, for the fused gate / up /
+    SwiGLU launch."""
+
+    def __init__(self, buf: torch.Tensor, n: int, k: int, bits: int):
+        self.buf, self.n, self.k, self.bits = buf, n, k, bits
+
+
+def qmm_pack_swiglu(gate, up, *, bits: int, group_size: int = GROUP) -> PackedSwiGLU:
+    """Pack (w, scales, biases) of the gate and of the up projection (same shape) into the pair
+    form once."""
+    (gw, gs, gb), (uw, us, ub) = gate, up
+    _require_cuda(gw, gs, gb, uw, us, ub)
+    _require_packed(gw)
+    _require_packed(uw)
+    if gw.shape != uw.shape or gs.shape != us.shape:
+        raise ValueError(f"gate {tuple(gw.shape)} and up {tuple(uw.shape)} must have one shape")
+    n, k = gw.shape[0], gw.shape[1] * 32 // bits
+    args = [t.contiguous() for t in (gw, gs, gb, uw, us, ub)]
+    lib = _lib.load()
+    nbytes = int(lib.dspark_qmm_swiglu_packed_bytes(n, k, bits, group_size))
+    if nbytes == 0:
+        raise _lib.DsparkError("dspark_qmm_pack_swiglu", -2, f"[{n}, {k}] {bits}-bit cannot be packed (K % 512 != 0)")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=gw.device)
+    _lib.call("dspark_qmm_pack_swiglu", *[_ptr(t) for t in args], n, k, bits, group_size, _ptr(buf), nbytes,
+              _stream(gw))
+    return PackedSwiGLU(buf, n, k, bits)
+
+
+def quantized_swiglu_packed(x: torch.Tensor, pair: PackedSwiGLU, *, group_size: int = GROUP,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(x W_gate^T) * (x W_up^T)`` with mlx's bf16 rounding, in one launch -> ``[.., N]``."""
+    _require_cuda(x, pair.buf)
+    _require_bf16("x", x)
+    k = x.shape[-1]
+    if k != pair.k:
+        raise ValueError(f"x has K={k}, the packed pair K={pair.k}")
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    h = out if out is not None else torch.empty((m, pair.n), dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    nbytes = lib.dspark_qmm_swiglu_packed_workspace(pair.n, k, m, pair.bits, group_size)
+    ws = qmm_workspace(x.device, nbytes)
+    _lib.call("dspark_qmm_swiglu_packed", _ptr(x2), x2.stride(0), _ptr(pair.buf), _ptr(h), h.stride(0), pair.n, k, m,
+              pair.bits, group_size, _ptr(ws), 0 if ws is None else ws.numel(), _stream(x))
+    return h.reshape(*x.shape[:-1], pair.n)
+
+
 def qmm_supported(m: int, k: int, n: int, bits: int, group_size: int = GROUP) -> bool:
     return _lib.load().dspark_qmm_affine_supported(m, k, n, bits, group_size) == 0
 

@@ -122,3 +122,82 @@ def test_refusals(dev):
     s = torch.zeros((64, 7), dtype=torch.bfloat16, device=dev)
     with pytest.raises(_lib.DsparkError):
         ops.qmm_pack(w, s, s, bits=8)
+
+
+# ---------------------------------------------------------------- fused gate / up / SwiGLU
+
+def _pair_np(gate, up, n, k, bits):
+    """The pair form from its definition: the packed layout of 2 ceil(n/16) tiles, gate tile t
+    then up tile t (weights section, then scale/bias section)."""
+    a, b = _pack_np(*gate, n, k, bits), _pack_np(*up, n, k, bits)
+    t, g = (n + 15) // 16, k // 64
+    wt = (g // 2 if bits == 4 else g) * 64 * 16     # weight bytes per tile
+    st = (g // 8) * 512                             # scale/bias bytes per tile
+    wa, wb = a[:t * wt].reshape(t, wt), b[:t * wt].reshape(t, wt)
+    sa, sb = a[t * wt:].reshape(t, st), b[t * wt:].reshape(t, st)
+    return np.concatenate([np.stack([wa, wb], 1).reshape(-1), np.stack([sa, sb], 1).reshape(-1)])
+
+
+@pytest.mark.parametrize("n,k,bits", [(40, 512, 8), (64, 1024, 4)])
+def test_swiglu_pair_layout(dev, n, k, bits):
+    from dspark_rocm import ops
+
+    gate, up = _quantized(n + 1, n, k, bits), _quantized(n + 2, n, k, bits)
+    pair = ops.qmm_pack_swiglu(_dev(*gate, dev), _dev(*up, dev), bits=bits)
+    assert np.array_equal(pair.buf.cpu().numpy(), _pair_np(gate, up, n, k, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("n,k", [(1024, 512), (4096, 4096), (640, 5120), (192, 25600)])
+@pytest.mark.parametrize("m", [1, 5, 16, 33])
+def test_swiglu_fused_is_bitwise_unfused(dev, bits, n, k, m):
+    """N a multiple of 64: the fused launch uses the same K slices as the two-problem launch, so
+    h equals SwiGLU(gate, up) of the unfused path bit for bit."""
+    import torch
+
+    from dspark_rocm import ops
+
+    gate, up = _quantized(3 * n + k + bits, n, k, bits), _quantized(5 * n + k + bits, n, k, bits)
+    gd, ud = _dev(*gate, dev), _dev(*up, dev)
+    x = randn_bf16(rng(m + 7 * n), m, k)
+    xd = to_dev_bf16(x, dev)
+    g, u = ops.quantized_matmul_packed_multi([xd], [ops.qmm_pack(*gd, bits=bits), ops.qmm_pack(*ud, bits=bits)])
+    want = ops.swiglu(g, u)
+    got = ops.quantized_swiglu_packed(xd, ops.qmm_pack_swiglu(gd, ud, bits=bits))
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("n,k,bits", [(40, 512, 8), (1000, 1024, 4), (24, 2048, 8)])
+def test_swiglu_fused_ragged_n_against_oracle(dev, n, k, bits):
+    """N not a multiple of 16 (padded tiles; other K slices than the unfused launch): h against
+    the oracle's SwiGLU of the oracle products, at the qmm bar."""
+    from oracle import moe_ref
+
+    from dspark_rocm import ops
+
+    gate, up = _quantized(n + 11, n, k, bits), _quantized(n + 12, n, k, bits)
+    x = randn_bf16(rng(n), 16, k)
+    h = ops.quantized_swiglu_packed(to_dev_bf16(x, dev), ops.qmm_pack_swiglu(_dev(*gate, dev), _dev(*up, dev),
+                                                                               bits=bits))
+    want = moe_ref.swiglu(qmm_ref.qmm_f64(x, *gate, bits), qmm_ref.qmm_f64(x, *up, bits))
+    assert_rms_close(from_dev_bf16(h), want, 2e-2, f"fused swiglu {bits}-bit [{n},{k}]")
+
+
+def test_swiglu_refusals(dev):
+    import torch
+
+    from dspark_rocm import _lib, ops
+
+    w = torch.zeros((64, 448 // 4), dtype=torch.int32, device=dev)
+    s = torch.zeros((64, 7), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_lib.DsparkError):                 # K % 512 != 0
+        ops.qmm_pack_swiglu((w, s, s), (w, s, s), bits=8)
+    w2 = torch.zeros((32, 512 // 4), dtype=torch.int32, device=dev)
+    s2 = torch.zeros((32, 8), dtype=torch.bfloat16, device=dev)
+    w3 = torch.zeros((64, 512 // 4), dtype=torch.int32, device=dev)
+    s3 = torch.zeros((64, 8), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):                       # gate and up shapes differ
+        ops.qmm_pack_swiglu((w2, s2, s2), (w3, s3, s3), bits=8)
+    pair = ops.qmm_pack_swiglu((w3, s3, s3), (w3, s3, s3), bits=8)
+    with pytest.raises(ValueError):                       # x with the wrong K
+        ops.quantized_swiglu_packed(torch.zeros((4, 1024), dtype=torch.bfloat16, device=dev), pair)

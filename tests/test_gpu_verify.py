@@ -186,14 +186,16 @@ def test_speculative_trace_is_lossless_with_expected_accept_length(dev):
 
 def test_packed_engine_is_bitwise_the_reference_layout_engine(dev):
     """The fused step reading every projection from the packed qmm form (hidden 512 and
-    intermediate 1024, so all seven projections and the lm_head are packable) produces the same
-    logits, bit for bit, as the step reading the reference layout, over blocks with rollback."""
+    intermediate 1024, so all seven projections and the lm_head are packable; gate and up as the
+    fused gate / up / SwiGLU pair) produces the same logits, bit for bit, as the step reading the
+    reference layout (gate, up and the SwiGLU kernel), over blocks with rollback."""
     from dspark_rocm.model import Target
 
     model = tiny_model(dev, seed=9, hidden_size=512, intermediate_size=1024)
     packed, plain = Target(model, packed=True), Target(model, packed=False)
-    n_mods = 7 * model.args.num_hidden_layers + 1
-    assert len(packed.engine._packed) == n_mods and not plain.engine._packed
+    layers = model.args.num_hidden_layers
+    assert len(packed.engine._packed) == 5 * layers + 1 and len(packed.engine._swiglu) == layers
+    assert not plain.engine._packed and not plain.engine._swiglu
     ca, cb = packed.make_cache(96), plain.make_cache(96)
     r = np.random.Generator(np.random.PCG64(4))
     for n, rej in ((16, 3), (7, 0), (16, 15)):
