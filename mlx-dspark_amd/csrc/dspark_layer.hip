@@ -83,6 +83,69 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const u16* x,
   }
 }
 
+// The same row op with every chunk of the row held in registers between the two phases: x, r
+// and w are all requested in one memory round trip, h is written once and never re-read.
+// Per-thread chunk order and the reductions match add_rmsnorm_kernel, so the results do too.
+template <int MAXC>
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_reg_kernel(const u16* x, long ldx, const u16* __restrict__ r,
+                                                                       long ldr, const u16* __restrict__ w, int H,
+                                                                       float eps, u16* hout, long ldh,
+                                                                       u16* __restrict__ y, long ldy) {
+  __shared__ float red[kNormThreads / 64];
+  const int m = blockIdx.x;
+  const u16* xr = x + (long)m * ldx;
+  const u16* rr = r ? r + (long)m * ldr : nullptr;
+  u16* hr = hout ? hout + (long)m * ldh : nullptr;
+  const int chunks = H >> 3;
+  u32x4_t hv[MAXC], rv[MAXC], wv[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = min((int)threadIdx.x + i * kNormThreads, chunks - 1);
+    hv[i] = ldg128(xr + 8 * c);
+    if (rr) rv[i] = ldg128(rr + 8 * c);
+    wv[i] = ldg128(w + 8 * c);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = threadIdx.x + i * kNormThreads;
+    if (c >= chunks) continue;
+    if (rr) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        hv[i][j] = pack_bf16x2(bf2f(hv[i][j] & 0xFFFFu) + bf2f(rv[i][j] & 0xFFFFu),
+                               bf2f(hv[i][j] >> 16) + bf2f(rv[i][j] >> 16));
+      if (hr) *reinterpret_cast<u32x4_t*>(hr + 8 * c) = hv[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf2f(hv[i][j] & 0xFFFFu), b = bf2f(hv[i][j] >> 16);
+      ss += a * a + b * b;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
+  const float inv = 1.0f / __builtin_sqrtf(tot / (float)H + eps);
+  u16* yr = y + (long)m * ldy;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = threadIdx.x + i * kNormThreads;
+    if (c >= chunks) continue;
+    u32x4_t out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf16r(bf2f(hv[i][j] & 0xFFFFu) * inv) * bf2f(wv[i][j] & 0xFFFFu);
+      const float b = bf16r(bf2f(hv[i][j] >> 16) * inv) * bf2f(wv[i][j] >> 16);
+      out[j] = pack_bf16x2(a, b);
+    }
+    *reinterpret_cast<u32x4_t*>(yr + 8 * c) = out;
+  }
+}
+
 struct QkArgs {
   const u16* q;
   const u16* k;
@@ -233,7 +296,8 @@ extern "C" int dspark_rmsnorm(const void* x, int64_t ldx, const void* r, int64_t
       (r && (!aligned(r, 16) || ldr % 8 || ldr < H)) || (h_out && (!aligned(h_out, 16) || ldh % 8 || ldh < H)))
     return fail(DSPARK_ERR_ALIGN, "rmsnorm: rows must be 16-byte aligned with strides %% 8 == 0 and >= H");
   if (h_out && !r) return fail(DSPARK_ERR_ARG, "rmsnorm: h_out needs a residual r");
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)M), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
+  auto norm = H <= 8 * kNormThreads * 4 ? add_rmsnorm_reg_kernel<4> : add_rmsnorm_kernel;
+  hipLaunchKernelGGL(norm, dim3((unsigned)M), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u16*>(x), (long)ldx, static_cast<const u16*>(r), (long)ldr,
                      static_cast<const u16*>(w), (int)H, eps, static_cast<u16*>(h_out), (long)ldh,
                      static_cast<u16*>(y), (long)ldy);

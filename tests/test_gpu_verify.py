@@ -28,14 +28,15 @@ def _np(t):
     return t.float().cpu().numpy()
 
 
-def test_rmsnorm_kernel(dev):
+@pytest.mark.parametrize("H", [5120, 8192, 8200, 16384])   # rows held in registers up to 8192
+def test_rmsnorm_kernel(dev, H):
     from dspark_rocm import ops
 
     g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    x = torch.randn((16, 5120), generator=g, device=dev).to(torch.bfloat16)
-    r = torch.randn((16, 5120), generator=g, device=dev).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(5120, generator=g, device=dev)).to(torch.bfloat16)
+    g.manual_seed(H)
+    x = torch.randn((16, H), generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn((16, H), generator=g, device=dev).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
     y = ops.rmsnorm(x, w, 1e-6)
     assert np.array_equal(_np(y), model_ref.rmsnorm(_np(x), _np(w), 1e-6)) or \
         np.abs(_np(y) - model_ref.rmsnorm(_np(x), _np(w), 1e-6)).max() <= 2 ** -7 * np.abs(_np(y)).max()
