@@ -88,6 +88,29 @@ def test_tree_mask(dev):
     assert_rms_close(out, ref, 2e-2, "tree")
 
 
+def _tree16(seed):
+    """Ancestor-or-self bits for a 16-row draft tree: row i's parent is a random earlier row."""
+    r = np.random.Generator(np.random.PCG64(seed))
+    anc = [1]
+    for i in range(1, 16):
+        anc.append(anc[int(r.integers(0, i))] | (1 << i))
+    return anc
+
+
+@pytest.mark.parametrize("hq,hk,L,d", [
+    (64, 8, 4112, 128),    # 128 rows per KV head: 8-wave workgroups, two tiles in flight
+    (64, 8, 1000, 64),     # same at head_dim 64, a short cache
+    (32, 8, 16400, 128),   # 64 rows, long cache: 4-wave workgroups
+    (32, 8, 600, 128),     # 64 rows, short cache: 8 waves splitting each tile's keys
+])
+def test_tree_mask_every_workgroup_shape(dev, hq, hk, L, d):
+    q, k, v = _mk(hq + L + d, 1, hq, hk, 16, L, d)
+    anc = _tree16(L)
+    out = _gpu(dev, q, k, v, L, d ** -0.5, False, tree_anc=anc)
+    ref = attn_ref.attention(q, k, v, d ** -0.5, tree_anc=anc)
+    assert_rms_close(out, ref, 2e-2, f"tree hq={hq} L={L} d={d}")
+
+
 @pytest.mark.parametrize("L", [512, 4096, 16384, 32768])
 def test_c3_lengths(dev, L):
     """C3: 32 q heads, 8 KV heads, D 128, 16 rows at offset L (L + 16 keys), split-KV."""
