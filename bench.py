@@ -7,9 +7,10 @@ launch, o, gate/up in one launch, down), rotating over a pool of distinct layers
 far past the 256 MB Infinity Cache) so every byte comes from HBM. The K timed steps are one
 HIP-graph replay bracketed by events. ``value`` = algorithmic bytes / measured time.
 
-Also reported under ``extra``: the single 4096x4096 qmm (4- and 8-bit, M = 1..16), 32k-context
-multi-row verify attention (32/8/128, 16 rows), and the 128-expert top-8 MoE block — each as
-µs per call and GB/s, chained over rotated pools.
+Also reported under ``extra``: the same layer set in 4-bit and read from the reference layout,
+the single 4096x4096 qmm (4- and 8-bit, M = 1..16), multi-row verify attention at 512..32k keys
+(32/8/128, 16 rows), the 128-expert top-8 MoE block and the 64-layer verify step at 16k context
+— each as µs per call and GB/s, chained over rotated pools.
 
 ``roofline`` is for the dominant kernel (the gate/up qmm launch): its algorithmic bytes over its
 average duration, taken from HIP events around that launch in an event-bracketed replay of the
@@ -99,7 +100,7 @@ def time_eager(fn, reps: int, warm: int = 3) -> float:
 # ------------------------------------------------------------------ workloads
 
 class LayerSet:
-    """C2: q/k/v/o/gate/up/down of an 8B-shaped layer, 8-bit g64, M rows; a pool of layers.
+    """C2: q/k/v/o/gate/up/down of an 8B-shaped layer, 8- or 4-bit g64, M rows; a pool of layers.
     Each matrix is held in the reference layout and in the packed qmm form (``ops.qmm_pack``);
     ``packed`` selects which one the launches read (the products are bit-identical)."""
 
@@ -446,7 +447,7 @@ def main() -> None:
         f"({time.perf_counter() - t0:.1f} s)")
 
     traffic = load_traffic()
-    roofline = {"kernel": "qmm_sk_kernel<8,4,16,true,true> gate+up launch, packed form (N=2x12288, K=4096, M=16; "
+    roofline = {"kernel": "qmm_sk_kernel<8,4,16,true,true,false> gate+up launch, packed form (N=2x12288, K=4096, M=16; "
                           "grid 384x4)", "bound": "hbm",
                 "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
@@ -472,6 +473,20 @@ def main() -> None:
                 extra["C1"].append(r)
                 log(f"C1 {b}-bit M={m}: {r['us_chained']} us chained ({r['GBs_chained']} GB/s), "
                     f"{r['us_single']} us single")
+        # the same 8B-shaped layer set quantized 4-bit (packed form): the 4-bit small-M qmm at a
+        # layer's size, where C1's single 4096 x 4096 matrix is launch-bound
+        ls4 = LayerSet(dev, 4, M, a.layers, seed=2)
+        ms4, _ = time_graph(lambda: [ls4.step(i) for i in range(K)], 1)
+        gu4, _ = time_graph(lambda: [ls4.gate_up(i) for i in range(K)], 1)
+        s4 = ms4 / K
+        extra["C2_4bit"] = {"step_us": round(s4 * 1e3, 3), "bytes_per_step": ls4.bytes_per_step,
+                            "GBs": round(ls4.bytes_per_step / (s4 * 1e-3) / 1e9, 1),
+                            "frac_of_peak": round(ls4.bytes_per_step / (s4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                            "gate_up_us": round(gu4 * 1e3 / K, 3),
+                            "gate_up_GBs": round(ls4.gu_bytes / (gu4 / K * 1e-3) / 1e9, 1)}
+        log(f"C2 4-bit: {s4 * 1e3:.2f} us/step ({extra['C2_4bit']['GBs']} GB/s), gate/up {gu4 * 1e3 / K:.2f} us "
+            f"({extra['C2_4bit']['gate_up_GBs']} GB/s)")
+        del ls4
         extra["C3"] = []
         for L in (512, 4096, 16384, 32768):
             r = bench_attention(dev, L)
