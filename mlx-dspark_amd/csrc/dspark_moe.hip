@@ -121,8 +121,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
         gsel[wave * 32 + j] = bf16r(expf(route_key_logit(m) - mx) / sum);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
+    // gsel is written and read by lane 0 only (in order; the compiler waits on the LDS
+    // dependency), so no wait on the global index stores is needed here
     if (lane == 0) {
       float gsum = 0.f;
       for (int j = 0; j < a.k; ++j) gsum += gsel[wave * 32 + j];

@@ -19,7 +19,7 @@ namespace dspark {
 
 constexpr int kQmmMaxProblems = DSPARK_QMM_MAX_PROBLEMS;
 constexpr int kQmmMaxSlices = 32;
-constexpr int kSliceChunk = 8;  // partials the last arriver requests at a time
+constexpr int kSliceChunk = 16;  // partials the last arriver requests at a time
 // buffer resource word 3 for gfx9-family raw buffers, and the sc1 (device-coherent) cache
 // policy of buffer loads and stores
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -412,8 +412,9 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     u32x4_t pv[kSliceChunk];
 #pragma unroll
     for (int s2 = 0; s2 < kSliceChunk; ++s2)
-      pv[s2] = __builtin_amdgcn_raw_buffer_load_b128(prs, ((min(s0 + s2, S - 1) * TW + col) * 16 + 4 * rq) * 4, 0,
-                                                     kCoherentSc1);
+      if (s0 + s2 < S)  // wave-uniform: no request past the last slice
+        pv[s2] = __builtin_amdgcn_raw_buffer_load_b128(prs, (((s0 + s2) * TW + col) * 16 + 4 * rq) * 4, 0,
+                                                       kCoherentSc1);
 #pragma unroll
     for (int s2 = 0; s2 < kSliceChunk; ++s2)
       if (s0 + s2 < S) v += __builtin_bit_cast(f32x4_t, pv[s2]);
