@@ -55,6 +55,14 @@ __device__ __forceinline__ float route_key_logit(u32 key) {
 }
 
 // Maximum of v over the wave: DPP within each row of 16 lanes, then the four row results.
+// Workgroup barrier for data exchanged through LDS: the fences are restricted to LDS, so a
+// wave waits for its LDS operations but not for its global stores.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ u32 wave_max_u32(u32 v) {
   v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
   v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
@@ -74,12 +82,10 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
   extern __shared__ int lds[];
   int* pair_e = lds;                                                 // [M*k]
   int* counts = lds + a.M * a.k;                                     // [kRouteThreads]
-  float* gsel = reinterpret_cast<float*>(counts + kRouteThreads);   // [16][32]
-  u32* tmask = reinterpret_cast<u32*>(gsel + 16 * 32);               // [2][kRouteThreads] token bits (M <= 64)
+  u32* tmask = reinterpret_cast<u32*>(counts + kRouteThreads);       // [2][kRouteThreads] token bits (M <= 64)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int P = a.M * a.k;
 
-  for (int i = threadIdx.x; i < a.nctr; i += kRouteThreads) a.ctr[i] = 0;
   counts[threadIdx.x] = 0;
   tmask[threadIdx.x] = 0;
   tmask[kRouteThreads + threadIdx.x] = 0;
@@ -88,10 +94,13 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     float xv[NPL];
     u32 key[NPL];
     u32 kmax = 0;
+    u16 lg[NPL];  // every lane's logits requested together (clamped index, no branch)
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) lg[i] = a.logits[(long)t * a.E + min(lane + 64 * i, a.E - 1)];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const int e = lane + 64 * i;
-      const u32 b = (e < a.E) ? (u32)a.logits[(long)t * a.E + e] : 0xFF80u;
+      const u32 b = (e < a.E) ? (u32)lg[i] : 0xFF80u;
       key[i] = (e < a.E) ? route_key(b, e) : 0u;  // every real key is > 0
       xv[i] = route_key_logit(key[i]);
       kmax = max(kmax, key[i]);
@@ -104,6 +113,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
       if (lane + 64 * i < a.E) sum += expf(xv[i] - mx);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += shfl_xor(sum, o);
+    u32 mine = 0;  // lane j < k keeps the key of slot j
     for (int j = 0; j < a.k; ++j) {
       if (j > 0) {
         kmax = 0;
@@ -115,39 +125,40 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
 #pragma unroll
       for (int i = 0; i < NPL; ++i)
         if (lane + 64 * i == e) key[i] = 0u;
-      if (lane == 0) {
-        a.inds[t * a.k + j] = e;
-        pair_e[t * a.k + j] = e;
-        gsel[wave * 32 + j] = bf16r(expf(route_key_logit(m) - mx) / sum);
-      }
+      if (lane == j) mine = m;
     }
-    // gsel is written and read by lane 0 only (in order; the compiler waits on the LDS
-    // dependency), so no wait on the global index stores is needed here
-    if (lane == 0) {
-      float gsum = 0.f;
-      for (int j = 0; j < a.k; ++j) gsum += gsel[wave * 32 + j];
-      const float denom = bf16r(gsum);
-      for (int j = 0; j < a.k; ++j) {
-        const float g = gsel[wave * 32 + j];
-        a.scores[t * a.k + j] = f2bf(a.renorm ? bf16r(g / denom) : g);
-      }
+    // lanes 0..k-1 finish their slots together: expert, gate value, and the renormalised
+    // score over the slot-order fp32 sum of the k gate values
+    const int e_mine = 0xFFFF - (int)(mine & 0xFFFFu);
+    const float g_mine = bf16r(expf(route_key_logit(mine) - mx) / sum);
+    float gsum = 0.f;
+    for (int j = 0; j < a.k; ++j) gsum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g_mine), j));
+    const float denom = bf16r(gsum);
+    if (lane < a.k) {
+      a.inds[t * a.k + lane] = e_mine;
+      pair_e[t * a.k + lane] = e_mine;
+      a.scores[t * a.k + lane] = f2bf(a.renorm ? bf16r(g_mine / denom) : g_mine);
     }
     __builtin_amdgcn_wave_barrier();
   }
+  // the grouped qmm's arrival counters (after the logits loads, which would otherwise wait
+  // behind these stores)
+  for (int i = threadIdx.x; i < a.nctr; i += kRouteThreads) a.ctr[i] = 0;
   if (!a.offsets) return;
   // ---- bucket the (token, slot) pairs by expert, stable in pair id. A token selects an
   // expert at most once, so a pair's place in its bucket is the number of earlier tokens that
-  // selected the same expert.
-  __syncthreads();
+  // selected the same expert. The phases share data through LDS only, so their barriers wait
+  // for LDS traffic and leave the global stores (indices, scores, counters) draining.
+  lds_barrier();
   const bool bits = a.M <= 64;
   for (int p = threadIdx.x; p < P; p += kRouteThreads) {
     const int pe = pair_e[p], t = p / a.k;
     if (bits) atomicOr(&tmask[(t >> 5) * kRouteThreads + pe], 1u << (t & 31));
     else atomicAdd(&counts[pe], 1);
   }
-  __syncthreads();
+  lds_barrier();
   if (bits) counts[threadIdx.x] = __builtin_popcount(tmask[threadIdx.x]) + __builtin_popcount(tmask[kRouteThreads + threadIdx.x]);
-  __syncthreads();
+  lds_barrier();
   // exclusive scan of the bucket sizes by wave 0, 64 experts at a time; counts[e] becomes the
   // bucket start
   if (wave == 0) {
@@ -169,7 +180,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     }
     if (lane == 0) a.offsets[a.E] = carry;
   }
-  __syncthreads();
+  lds_barrier();
   for (int p = threadIdx.x; p < P; p += kRouteThreads) {
     const int pe = pair_e[p], t = p / a.k;
     int before = 0;
@@ -356,7 +367,7 @@ int check_route(long M, long E, long k) {
 }
 
 int launch_route(const RouteArgs& a, hipStream_t s) {
-  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + 3 * kRouteThreads + 16 * 32);
+  const size_t lds = sizeof(int) * ((size_t)a.M * a.k + 3 * kRouteThreads);
   const dim3 g(1), b(kRouteThreads);
   if (a.E <= 64) hipLaunchKernelGGL(moe_route_kernel<1>, g, b, lds, s, a);
   else if (a.E <= 128) hipLaunchKernelGGL(moe_route_kernel<2>, g, b, lds, s, a);
