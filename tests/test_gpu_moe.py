@@ -99,3 +99,9 @@ def test_switch_glu(dev, M, E, k, H, I, bits):
     ref, ri, rs = moe_ref.switch_glu(x, logits, *g, *u, *d, k=k, bits=bits)
     assert np.array_equal(inds.cpu().numpy(), ri)
     assert_rms_close(from_dev_bf16(out), ref, 2e-2, "switch_glu")
+    # a second call gives the same bits (the combine's arrival counters were left at zero)
+    out2, _, _ = ops.moe_switch_glu(to_dev_bf16(x, dev), to_dev_bf16(logits, dev), _dev3(g, dev), _dev3(u, dev),
+                                    _dev3(d, dev), k=k, bits=bits)
+    import torch
+
+    assert torch.equal(out2, out)
