@@ -55,14 +55,6 @@ __device__ __forceinline__ float route_key_logit(u32 key) {
 }
 
 // Maximum of v over the wave: DPP within each row of 16 lanes, then the four row results.
-// Workgroup barrier for data exchanged through LDS: the fences are restricted to LDS, so a
-// wave waits for its LDS operations but not for its global stores.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ u32 wave_max_u32(u32 v) {
   v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
   v = max(v, (u32)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
@@ -147,18 +139,17 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
   if (!a.offsets) return;
   // ---- bucket the (token, slot) pairs by expert, stable in pair id. A token selects an
   // expert at most once, so a pair's place in its bucket is the number of earlier tokens that
-  // selected the same expert. The phases share data through LDS only, so their barriers wait
-  // for LDS traffic and leave the global stores (indices, scores, counters) draining.
-  lds_barrier();
+  // selected the same expert.
+  __syncthreads();
   const bool bits = a.M <= 64;
   for (int p = threadIdx.x; p < P; p += kRouteThreads) {
     const int pe = pair_e[p], t = p / a.k;
     if (bits) atomicOr(&tmask[(t >> 5) * kRouteThreads + pe], 1u << (t & 31));
     else atomicAdd(&counts[pe], 1);
   }
-  lds_barrier();
+  __syncthreads();
   if (bits) counts[threadIdx.x] = __builtin_popcount(tmask[threadIdx.x]) + __builtin_popcount(tmask[kRouteThreads + threadIdx.x]);
-  lds_barrier();
+  __syncthreads();
   // exclusive scan of the bucket sizes by wave 0, 64 experts at a time; counts[e] becomes the
   // bucket start
   if (wave == 0) {
@@ -180,7 +171,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     }
     if (lane == 0) a.offsets[a.E] = carry;
   }
-  lds_barrier();
+  __syncthreads();
   for (int p = threadIdx.x; p < P; p += kRouteThreads) {
     const int pe = pair_e[p], t = p / a.k;
     int before = 0;
