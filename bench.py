@@ -100,7 +100,8 @@ def time_eager(fn, reps: int, warm: int = 3) -> float:
 # ------------------------------------------------------------------ workloads
 
 class LayerSet:
-    """C2: q/k/v/o/gate/up/down of an 8B-shaped layer, 8- or 4-bit g64, M rows; a pool of layers.
+    """The projection set of an 8B-shaped layer: q/k/v/o/gate/up/down, 8- or 4-bit g64, M rows; a
+    pool of layers.
     Each matrix is held in the reference layout and in the packed qmm form (``ops.qmm_pack``);
     ``packed`` selects which one the launches read (the products are bit-identical)."""
 
@@ -166,7 +167,7 @@ class LayerSet:
 
 
 def bench_qmm_single(dev, bits: int, m: int, n: int = 4096, k: int = 4096, reps: int = 200):
-    """C1: one [n, k] qmm, single launch (cold from HBM) and chained over a >= 1 GB pool."""
+    """One [n, k] qmm, single launch (cold from HBM) and chained over a >= 1 GB pool."""
     import torch
 
     from dspark_rocm import ops
@@ -211,7 +212,7 @@ def bench_qmm_single(dev, bits: int, m: int, n: int = 4096, k: int = 4096, reps:
 
 
 def bench_attention(dev, L: int, hq=32, hk=8, d=128, mq=16, reps: int = 50):
-    """C3: 16 verify rows over L cached keys (+ the 16 new rows), rotated KV sets >= 1 GB."""
+    """Verify attention: 16 rows over L cached keys (+ the 16 new rows), rotated KV sets >= 1 GB."""
     import torch
 
     from dspark_rocm import ops
@@ -243,7 +244,7 @@ def bench_attention(dev, L: int, hq=32, hk=8, d=128, mq=16, reps: int = 50):
 
 
 def bench_moe(dev, m=16, E=128, k=8, H=2048, I=768, bits=4, reps: int = 30):
-    """C4: routed-expert block (route + gate/up + down + combine) over rotated expert pools."""
+    """The routed-expert block (route + gate/up + down + combine) over rotated expert pools."""
     import torch
 
     from dspark_rocm import ops
@@ -277,7 +278,7 @@ def bench_moe(dev, m=16, E=128, k=8, H=2048, I=768, bits=4, reps: int = 30):
 
 
 def bench_verify_forward(dev, context: int = 16384, rows: int = 16, reps: int = 10):
-    """C5: one speculative verify step of a random-init dense 8-bit 64-layer target (hidden
+    """One speculative verify step of a random-init dense 8-bit 64-layer target (hidden
     5120, heads 64/8 x 128, intermediate 25600, vocab 151936, RoPE 1e6) with `rows` verify rows
     over a `context`-row synthetic bf16 KV cache: the forward, lm_head, device argmax and
     greedy accept, captured as one hipGraph (the KV write lands at the same positions each
@@ -374,7 +375,7 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=8, help="distinct layers in the rotated pool")
-    ap.add_argument("--quick", action="store_true", help="skip the C1/C3/C4 extras and the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="skip the single-qmm, attention and MoE extras and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c5", action="store_true", help="skip the full 64-layer verify-forward extra")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -394,9 +395,9 @@ def main() -> None:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     M, bits = 16, 8
-    log(f"device {torch.cuda.get_device_name(dev)}; building C2 pool of {a.layers} layers")
+    log(f"device {torch.cuda.get_device_name(dev)}; building the layer-set pool of {a.layers} layers")
     ls = LayerSet(dev, bits, M, a.layers)
-    log(f"C2 pool: {ls.weight_bytes * a.layers / 1e9:.2f} GB weights; step bytes {ls.bytes_per_step}")
+    log(f"layer-set pool: {ls.weight_bytes * a.layers / 1e9:.2f} GB weights; step bytes {ls.bytes_per_step}")
 
     if a.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -433,7 +434,7 @@ def main() -> None:
     ms_total = e0.elapsed_time(e1)
     ms_step = ms_total / K
     gbs = ls.bytes_per_step / (ms_step * 1e-3) / 1e9
-    log(f"C2 graph: {ms_step * 1e3:.2f} us/step, {gbs:.1f} GB/s")
+    log(f"layer-set graph: {ms_step * 1e3:.2f} us/step, {gbs:.1f} GB/s")
 
     # eager, for reference (host-issue bound at these sizes)
     t0 = time.perf_counter()
@@ -454,51 +455,51 @@ def main() -> None:
                 "traffic": (traffic or {}).get("qmm_gate_up_bytes"),
                 "bytes_per_launch": ls.gu_bytes, "avg_launch_us": round(gu_avg * 1e3, 3)}
 
-    extra = {"C2_step_us": round(ms_step * 1e3, 3), "C2_eager_step_us": round(eager_ms * 1e3, 3),
-             "C2_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    extra = {"layer_set_step_us": round(ms_step * 1e3, 3), "layer_set_eager_step_us": round(eager_ms * 1e3, 3),
+             "layer_set_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if not a.quick:
         # the same set read from the reference layout (what a drop-in caller passes per call)
         ls.packed = False
         ref_ms, _ = time_graph(lambda: [ls.step(i) for i in range(K)], 1)
         ref_gu, _ = time_graph(lambda: [ls.gate_up(i) for i in range(K)], 1)
         ls.packed = True
-        extra["C2_reference_layout"] = {"step_us": round(ref_ms * 1e3 / K, 3),
+        extra["layer_set_reference_layout"] = {"step_us": round(ref_ms * 1e3 / K, 3),
                                         "GBs": round(ls.bytes_per_step / (ref_ms / K * 1e-3) / 1e9, 1),
                                         "gate_up_us": round(ref_gu * 1e3 / K, 3)}
-        log(f"C2 reference layout: {ref_ms * 1e3 / K:.2f} us/step, gate/up {ref_gu * 1e3 / K:.2f} us")
-        extra["C1"] = []
+        log(f"layer set, reference layout: {ref_ms * 1e3 / K:.2f} us/step, gate/up {ref_gu * 1e3 / K:.2f} us")
+        extra["qmm_4096x4096"] = []
         for b in (4, 8):
             for m in (1, 2, 4, 8, 16):
                 r = bench_qmm_single(dev, b, m)
-                extra["C1"].append(r)
-                log(f"C1 {b}-bit M={m}: {r['us_chained']} us chained ({r['GBs_chained']} GB/s), "
+                extra["qmm_4096x4096"].append(r)
+                log(f"qmm 4096x4096 {b}-bit M={m}: {r['us_chained']} us chained ({r['GBs_chained']} GB/s), "
                     f"{r['us_single']} us single")
         # the same 8B-shaped layer set quantized 4-bit (packed form): the 4-bit small-M qmm at a
-        # layer's size, where C1's single 4096 x 4096 matrix is launch-bound
+        # layer's size, where the single 4096 x 4096 matrix is launch-bound
         ls4 = LayerSet(dev, 4, M, a.layers, seed=2)
         ms4, _ = time_graph(lambda: [ls4.step(i) for i in range(K)], 1)
         gu4, _ = time_graph(lambda: [ls4.gate_up(i) for i in range(K)], 1)
         s4 = ms4 / K
-        extra["C2_4bit"] = {"step_us": round(s4 * 1e3, 3), "bytes_per_step": ls4.bytes_per_step,
+        extra["layer_set_4bit"] = {"step_us": round(s4 * 1e3, 3), "bytes_per_step": ls4.bytes_per_step,
                             "GBs": round(ls4.bytes_per_step / (s4 * 1e-3) / 1e9, 1),
                             "frac_of_peak": round(ls4.bytes_per_step / (s4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                             "gate_up_us": round(gu4 * 1e3 / K, 3),
                             "gate_up_GBs": round(ls4.gu_bytes / (gu4 / K * 1e-3) / 1e9, 1)}
-        log(f"C2 4-bit: {s4 * 1e3:.2f} us/step ({extra['C2_4bit']['GBs']} GB/s), gate/up {gu4 * 1e3 / K:.2f} us "
-            f"({extra['C2_4bit']['gate_up_GBs']} GB/s)")
+        log(f"layer set 4-bit: {s4 * 1e3:.2f} us/step ({extra['layer_set_4bit']['GBs']} GB/s), gate/up {gu4 * 1e3 / K:.2f} us "
+            f"({extra['layer_set_4bit']['gate_up_GBs']} GB/s)")
         del ls4
-        extra["C3"] = []
+        extra["verify_attention"] = []
         for L in (512, 4096, 16384, 32768):
             r = bench_attention(dev, L)
-            extra["C3"].append(r)
-            log(f"C3 L={L}: {r['us_chained']} us ({r['GBs_chained']} GB/s), NB={r['blocks']}")
+            extra["verify_attention"].append(r)
+            log(f"verify attention L={L}: {r['us_chained']} us ({r['GBs_chained']} GB/s), NB={r['blocks']}")
         r = bench_moe(dev)
-        extra["C4"] = r
-        log(f"C4 MoE: {r['us_chained']} us ({r['GBs_chained']} GB/s), {r['distinct_experts']} experts")
+        extra["moe_block"] = r
+        log(f"MoE block: {r['us_chained']} us ({r['GBs_chained']} GB/s), {r['distinct_experts']} experts")
         if not a.no_c5:
             r = bench_verify_forward(dev)
-            extra["C5"] = r
-            log(f"C5 verify step (64 layers, 16 rows @ 16k): {r['ms_graph']} ms ({r['GBs']} GB/s, "
+            extra["verify_step"] = r
+            log(f"verify step (64 layers, 16 rows @ 16k): {r['ms_graph']} ms ({r['GBs']} GB/s, "
                 f"{r['frac_of_peak']:.1%} of peak), {r['bytes'] / 1e9:.2f} GB/step; built in {r['build_s']} s")
             torch.cuda.empty_cache()
 

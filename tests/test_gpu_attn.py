@@ -4,7 +4,7 @@ Bar: max|Δ| <= 2e-2 * RMS(out) against the float64 definition; additionally wit
 ulps of the restatement of the multirow kernel's arithmetic (bf16 P, fp32 partials). Cases
 follow the reference's tests/test_multirow_attn.py:48-99 (GQA 1..16, off-grid KV lengths,
 strided cache views, batch 2, row groups, causal and bidirectional, the causal leak KAT), plus
-the tree mask, the C3 shapes and KV rollback r in {0, 5, 15}.
+the tree mask, the 32/8-head verify shapes at L = 512..32k and KV rollback r in {0, 5, 15}.
 """
 
 from __future__ import annotations
@@ -40,7 +40,7 @@ def _gpu(dev, q, k, v, L, scale, causal, tree_anc=None):
 
 CASES = [
     # B, hq, hk, q_len, L, d
-    (1, 32, 8, 16, 528, 128),     # C3 at L = 512 (+16 verify rows)
+    (1, 32, 8, 16, 528, 128),     # 32/8 heads, D 128 at L = 512 (+16 verify rows)
     (1, 32, 8, 15, 777, 128),     # DSpark drafter block, off-grid tail
     (1, 32, 8, 2, 64, 128),
     (1, 32, 2, 16, 500, 128),     # GQA 16 -> 256 rows: 4 row groups
@@ -113,14 +113,14 @@ def test_tree_mask_every_workgroup_shape(dev, hq, hk, L, d):
 
 @pytest.mark.parametrize("L", [512, 4096, 16384, 32768])
 def test_c3_lengths(dev, L):
-    """C3: 32 q heads, 8 KV heads, D 128, 16 rows at offset L (L + 16 keys), split-KV."""
+    """32 q heads, 8 KV heads, D 128, 16 rows at offset L (L + 16 keys), split-KV."""
     from dspark_rocm import ops
 
     Lt = L + 16
     q, k, v = _mk(L, 1, 32, 8, 16, Lt, 128)
     out = _gpu(dev, q, k, v, Lt, 128 ** -0.5, True)
     ref = c_oracle.attention(quant_ref.bf16_bits(q), quant_ref.bf16_bits(k), quant_ref.bf16_bits(v), 128 ** -0.5, True)
-    assert_rms_close(out, ref, 2e-2, f"C3 L={L}")
+    assert_rms_close(out, ref, 2e-2, f"verify attention L={L}")
     assert ops.verify_attention_blocks(1, 32, 8, 16, 128, Lt) >= 1
 
 

@@ -4,7 +4,7 @@ path under the reference's own contracts:
 - small_m_matmul: inside the window the kernel serves the call, within
   ``0.02 * max(max|stock|, 1)`` of the stock path (small_m_qmm.py:120); outside it the result
   is the stock path bit for bit (tests/test_small_m_qmm.py:94-104);
-- multirow_attention: an eligible causal / tree call equals the oracle within the C3 tolerance;
+- multirow_attention: an eligible causal / tree call equals the oracle within the attention tolerance;
   an ineligible call falls through unchanged (multirow_attn.py:338-370);
 - gather_qmm / SwitchGLU / SparseMoeBlock against the MoE oracle (sorted and unsorted pairs).
 """

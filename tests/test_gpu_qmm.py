@@ -3,7 +3,7 @@
 Bar: max|Δ| <= 2e-2 * RMS(y) (bf16 out, fp32 accumulate); in practice the kernel lands within
 a couple of bf16 ulps, which the tighter per-element check below pins. Structure mirrors the
 reference's tests/test_small_m_qmm.py: every M of the window at both widths (:59-87), bitwise
-row-count invariance (:107-119), ragged N, the refusal paths, plus the full-size C1 shape.
+row-count invariance (:107-119), ragged N, the refusal paths, plus the full-size 4096 x 4096 shape.
 """
 
 from __future__ import annotations
@@ -81,11 +81,11 @@ def test_more_than_16_rows(dev, bits):
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_c1_full_size_against_c_oracle(dev, bits):
-    """C1: M=16, N=K=4096 (the C restatement, fp32 factored like the kernel)."""
+    """M=16, N=K=4096 (the C restatement, fp32 factored like the kernel)."""
     x, w, s, b = _problem(0, 16, 4096, 4096, bits)
     got = _run(dev, x, w, s, b, bits)
     ref = c_oracle.qmm(quant_ref.bf16_bits(x), w, quant_ref.bf16_bits(s), quant_ref.bf16_bits(b), bits)
-    _check(got, ref.astype(np.float64), f"C1 {bits}-bit")
+    _check(got, ref.astype(np.float64), f"4096x4096 {bits}-bit")
 
 
 @pytest.mark.parametrize("bits", [4, 8])

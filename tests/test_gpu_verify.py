@@ -1,4 +1,4 @@
-"""GPU: the dense verify forward (C5's path) against the oracle.
+"""GPU: the dense verify forward (the 64-layer verify step's path) against the oracle.
 
 - layer kernels (residual + RMSNorm, q/k norm + RoPE + cache write, SwiGLU, argmax, greedy
   accept) against oracle/model_ref.py, moe_ref.swiglu and verify_ref (bit-exact for indices);

@@ -118,7 +118,7 @@ def test_multirow_plan_kats():
     from dspark_rocm import _lib
     from dspark_rocm.multirow_attn import plan
 
-    p = plan(32, 8, 16, 128, 32784)                  # C3 at 32k: 64 rows of one KV head
+    p = plan(32, 8, 16, 128, 32784)                  # 32/8 heads at 32k: 64 rows of one KV head
     assert (p["R"], p["RP"], p["NRG"]) == (64, 64, 1)
     assert p["CHUNK"] % 64 == 0 and p["NB"] * p["CHUNK"] >= 32784 > (p["NB"] - 1) * p["CHUNK"]
     assert p["workgroups"] == 8 * p["NB"]
@@ -363,7 +363,7 @@ def test_roofline_math():
     mbu = R.baseline_mbu(2.0, 8_000_000_000, 8000.0)
     assert mbu["achieved_gb_s"] == 4000.0 and mbu["mbu"] == 0.5
     assert R.baseline_mbu(0, 1, 1.0) is None
-    # the byte formulas the bench quotes
+    # the byte formulas the bench quotes (the single 4096² qmm, 32k verify attention, the A3B MoE block)
     assert R.qmm_bytes(4096, 4096, 4, 16) == 9_699_328
     assert R.qmm_bytes(4096, 4096, 8, 16) == 18_087_936
     assert R.attention_bytes(32, 8, 128, 16, 32768 + 16) == 4096 * (32768 + 16) + 262_144
