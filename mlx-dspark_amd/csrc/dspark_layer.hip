@@ -246,14 +246,24 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const u16* 
   float best = -INFINITY;
   int bid = 0x7FFFFFFF;
   const int chunks = V >> 3;
-  for (int c = threadIdx.x; c < chunks; c += kArgmaxThreads) {
-    const u32x4_t v = ldg128(row + 8 * c);
+  // four chunks requested per round trip (the selection is order-independent: a strict order on
+  // (value, -index), NaN never selected)
+  auto take = [&](const u32x4_t v, int c) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       arg_better(best, bid, bf2f(v[i] & 0xFFFFu), 8 * c + 2 * i);
       arg_better(best, bid, bf2f(v[i] >> 16), 8 * c + 2 * i + 1);
     }
+  };
+  int c = threadIdx.x;
+  for (; c + 3 * kArgmaxThreads < chunks; c += 4 * kArgmaxThreads) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = ldg128(row + 8 * (c + u * kArgmaxThreads));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) take(v[u], c + u * kArgmaxThreads);
   }
+  for (; c < chunks; c += kArgmaxThreads) take(ldg128(row + 8 * c), c);
   for (int j = 8 * chunks + threadIdx.x; j < V; j += kArgmaxThreads) arg_better(best, bid, bf2f(row[j]), j);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
