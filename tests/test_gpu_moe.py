@@ -85,6 +85,7 @@ def _dev3(t, dev):
 
 @pytest.mark.parametrize("M,E,k,H,I,bits", [(16, 8, 2, 256, 128, 4), (5, 16, 4, 512, 192, 8),
                                              (16, 128, 8, 2048, 768, 4),
+                                             (16, 128, 8, 2048, 768, 8),  # the A3B block with 8-bit experts
                                              (16, 2, 2, 512, 256, 4),     # every token in both experts: 16-row buckets
                                              (33, 4, 2, 256, 4096, 8)])   # 3 row tiles; down K = 4096 in 4 K parts
 def test_switch_glu(dev, M, E, k, H, I, bits):

@@ -54,7 +54,8 @@ def test_window_numerics(dev, bits, m):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("k,n", [(64, 8), (192, 72), (256, 64), (768, 2048), (2048, 768), (12288, 128)])
+@pytest.mark.parametrize("k,n", [(64, 8), (192, 72), (256, 64), (768, 2048), (2048, 768), (12288, 128),
+                                 (32768, 96)])   # the largest K: 32 slices of 16 groups
 def test_shapes(dev, bits, k, n):
     x, w, s, b = _problem(7 * k + n, 16, k, n, bits)
     got = _run(dev, x, w, s, b, bits)
