@@ -77,6 +77,7 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
   constexpr int LOADS = KT * DC / THREADS;  // 16-byte K chunks per thread per tile
   constexpr int NDC = D / 32;         // d-chunks of the S MFMA
   constexpr int NDT = D / 16;         // d-tiles of the O MFMA
+  constexpr int VW = 4;               // V fragments requested ahead of their MFMAs
   // K tile, then the transposed V tile; reused for the key-half merge after the last tile
   __shared__ __attribute__((aligned(16))) u16 smem[KT * KP + D * KT];
   u16* const ks_lds = smem;
@@ -197,6 +198,17 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
         s[j] = mfma16x16x32(kf, qf[c], s[j]);
       }
     }
+    // V fragments of the P.V product (fragment f = (d-tile f / NU, key half f % NU)): the first
+    // VW are requested now, before the softmax, and each use requests the one VW further on,
+    // so the LDS latency hides behind the softmax and the MFMAs instead of stalling each pair
+    constexpr int NVF = NDT * NU;
+    auto vfrag = [&](int f) {
+      const int d = 16 * (f / NU) + c16, u = f % NU;
+      return *reinterpret_cast<const u32x4_t*>(&vt_lds[vt_off(d, 32 * (kh * NU + u) + 8 * q4)]);
+    };
+    u32x4_t vwin[VW];
+#pragma unroll
+    for (int f = 0; f < VW; ++f) vwin[f] = vfrag(f);
     // row max of the raw scores (invisible keys -inf; only a chunk's last tile, the causal
     // diagonal and the tree block need the mask). The scale is applied in the exponent:
     // p = 2^(s * scale - m) with m the running max of the scaled scores.
@@ -259,14 +271,12 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
       for (int t = 0; t < NDT; ++t) o[t] *= alpha;
     }
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const int d = 16 * t + c16;
-#pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(&vt_lds[vt_off(d, 32 * (kh * NU + u) + 8 * q4)]);
-        o[t] = mfma16x16x32(vf, ph[u], o[t]);
-        o[t] = mfma16x16x32(vf, pl[u], o[t]);
-      }
+    for (int f = 0; f < NVF; ++f) {
+      const int t = f / NU, u = f % NU;
+      const u32x4_t vf = vwin[f % VW];
+      if (f + VW < NVF) vwin[f % VW] = vfrag(f + VW);
+      o[t] = mfma16x16x32(vf, ph[u], o[t]);
+      o[t] = mfma16x16x32(vf, pl[u], o[t]);
     }
   };
 
