@@ -79,9 +79,10 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
   constexpr int NDT = D / 16;         // d-tiles of the O MFMA
   constexpr int VW = 4;               // V fragments requested ahead of their MFMAs
   // K tile, then the transposed V tile; reused for the key-half merge after the last tile
-  __shared__ __attribute__((aligned(16))) u16 smem[KT * KP + D * KT];
-  u16* const ks_lds = smem;
-  u16* const vt_lds = smem + KT * KP;
+  // two tile buffers: tile i is staged into buffer i & 1 while the other buffer may still be in
+  // use by waves finishing tile i - 1, so one barrier per tile suffices
+  constexpr int TILE = KT * KP + D * KT;
+  __shared__ __attribute__((aligned(16))) u16 smem[2 * TILE];
   static_assert(KS == 1 || (WV * 64 * NDT * 4 + 2 * WV * 16) * 4 <= (KT * KP + D * KT) * 2, "merge area");
 
   const int bh = blockIdx.x;
@@ -164,7 +165,9 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
   const u32 sel_lo = 0x05040100u, sel_hi = 0x07060302u;
   const u32 vsel_even = (vdc & 1) ? sel_hi : sel_lo;  // e even
   const u32 vsel_odd = (vdc & 1) ? sel_lo : sel_hi;   // e odd
-  auto store_tile = [&](const TileRegs& r) {
+  auto store_tile = [&](const TileRegs& r, int b) {
+    u16* const ks_lds = smem + b * TILE;
+    u16* const vt_lds = ks_lds + KT * KP;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int c = tid + THREADS * j;
@@ -184,7 +187,9 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
     }
   };
 
-  auto compute_tile = [&](int kt) {
+  auto compute_tile = [&](int kt, int b) {
+    const u16* const ks_lds = smem + b * TILE;
+    const u16* const vt_lds = ks_lds + KT * KP;
     // S^T[key][row] for this wave's NKS subtiles of 16 keys (keys 16 (ks0 + j) ..)
     const int ks0 = kh * NKS;
     f32x4_t s[NKS];
@@ -283,21 +288,20 @@ __global__ __launch_bounds__(64 * WV * KS) void attn_p1_kernel(const AttnArgs a)
   // PF tiles in flight: tile kt is staged from the registers its load landed in, which then
   // take the load of tile kt + PF*KT while tile kt is computed.
   TileRegs r0, r1;
-  auto step = [&](TileRegs& r, int kt) {
-    __syncthreads();  // previous tile fully consumed
-    store_tile(r);
-    __syncthreads();
+  auto step = [&](TileRegs& r, int kt, int b) {
+    store_tile(r, b);
+    __syncthreads();  // tile visible; every wave is done with the tile before (other buffer)
     if (kt + PF * KT < k1) load_tile(r, kt + PF * KT);
-    if (active) compute_tile(kt);
+    if (active) compute_tile(kt, b);
   };
   if (k0 < k1) load_tile(r0, k0);
   if constexpr (PF == 1) {
-    for (int kt = k0; kt < k1; kt += KT) step(r0, kt);
+    for (int kt = k0; kt < k1; kt += KT) step(r0, kt, ((kt - k0) / KT) & 1);
   } else {
     if (k0 + KT < k1) load_tile(r1, k0 + KT);
     for (int kt = k0; kt < k1; kt += 2 * KT) {
-      step(r0, kt);
-      if (kt + KT < k1) step(r1, kt + KT);
+      step(r0, kt, 0);
+      if (kt + KT < k1) step(r1, kt + KT, 1);
     }
   }
   // ---- finalize: lane (row c16, quarter q4) holds O^T[16t + 4q4 + i][row]
