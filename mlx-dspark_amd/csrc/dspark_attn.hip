@@ -14,8 +14,8 @@
 //     when there are at most 128), so each K/V byte is read from HBM once and shared by every
 //     query head of the GQA group. On short caches (few blocks) the 4 row tiles are worked by
 //     8 waves, two per tile splitting its keys.
-//   * 64-key tiles are staged through LDS from registers loaded one (4-wave workgroups) or two
-//     (8-wave workgroups) tiles ahead: K row-major (padded rows), V transposed (key-contiguous,
+//   * 64-key tiles are staged through two alternating LDS buffers (one barrier per tile) from
+//     registers loaded one (4-wave workgroups) or two (8-wave workgroups) tiles ahead: K row-major (padded rows), V transposed (key-contiguous,
 //     8-key blocks XOR-swizzled by d) because the P.V MFMA reduces over keys.
 //   * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16. Computing the transposed
 //     scores leaves each lane holding 8 keys of one query row, which is exactly the B operand
