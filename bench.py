@@ -382,7 +382,7 @@ def main() -> None:
     ap.add_argument("--layers", type=int, default=8, help="distinct layers in the rotated pool")
     ap.add_argument("--quick", action="store_true", help="skip the single-qmm, attention and MoE extras and the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-c5", action="store_true", help="skip the full 64-layer verify-forward extra")
+    ap.add_argument("--no-verify-step", action="store_true", help="skip the full 64-layer verify-forward extra")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (for scaling rocprof byte counters)")
     a = ap.parse_args()
@@ -501,7 +501,7 @@ def main() -> None:
         r = bench_moe(dev)
         extra["moe_block"] = r
         log(f"MoE block: {r['us_chained']} us ({r['GBs_chained']} GB/s), {r['distinct_experts']} experts")
-        if not a.no_c5:
+        if not a.no_verify_step:
             r = bench_verify_forward(dev)
             extra["verify_step"] = r
             log(f"verify step (64 layers, 16 rows @ 16k): {r['ms_graph']} ms ({r['GBs']} GB/s, "

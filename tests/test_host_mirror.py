@@ -369,3 +369,18 @@ def test_roofline_math():
     assert R.attention_bytes(32, 8, 128, 16, 32768 + 16) == 4096 * (32768 + 16) + 262_144
     assert R.moe_bytes(1, 2048, 768, 4, 16, 128) == 2_654_208 + 135_168
     assert R.kv_bytes_per_token(64, 8, 128) == 64 * 4096
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 (or a WORLD_SIZE above 1) exits with a message
+    before touching a device."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
