@@ -48,10 +48,11 @@ def test_rmsnorm_kernel(dev, H):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-def test_qk_norm_rope_kv_kernel(dev, D):
+@pytest.mark.parametrize("Hq,Hk", [(8, 2), (5, 1)])   # 5 + 2 heads: a partly filled workgroup
+def test_qk_norm_rope_kv_kernel(dev, D, Hq, Hk):
     from dspark_rocm import ops
 
-    M, Hq, Hk, pos0, cap = 16, 8, 2, 16384, 16384 + 64
+    M, pos0, cap = 16, 16384, 16384 + 64
     g = torch.Generator(device=dev)
     g.manual_seed(D)
     q = torch.randn((M, Hq * D), generator=g, device=dev).to(torch.bfloat16)
