@@ -425,7 +425,7 @@ def main() -> None:
     with torch.cuda.stream(s):
         ls.step(0)
     torch.cuda.synchronize()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for i in range(K):
             ls.step(i)
     g.replay()  # warm replay

@@ -80,6 +80,13 @@ int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t K,
 /* Workspace bytes dspark_qmm_affine needs for this shape (0 = none). */
 size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, int bits, int group_size);
 
+/* Clears the split-K arrival counters of a qmm workspace (its first 256 KiB, or all of it when
+ * smaller) with a fill kernel on `stream`, so the call may sit in a captured graph. Every qmm
+ * call that completes leaves its counters at zero; this restores the invariant after a call
+ * that did not complete, or for a workspace of unknown contents. No counterpart in the
+ * reference, whose Metal kernel keeps no state between launches (skinny_qmm.py:56-159). */
+int dspark_qmm_workspace_reset(void* workspace, size_t workspace_bytes, dspark_stream stream);
+
 /* 0 if dspark_qmm_affine accepts this shape, else the dspark_status it would return.
  * Mirrors skinny_qmm.fits (skinny_qmm.py:174-181) without launching. */
 int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int bits, int group_size);

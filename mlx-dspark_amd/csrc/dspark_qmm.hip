@@ -493,3 +493,28 @@ extern "C" int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t 
   dspark_qmm_problem p{x, ldx, w, scales, biases, y, ldy, N, K};
   return dspark_qmm_affine_multi(&p, 1, M, bits, group_size, workspace, workspace_bytes, stream);
 }
+
+// ---- split-K counter reset: a fill kernel (not hipMemsetAsync, so the call may sit in a
+// captured graph) over the counter region at the start of a qmm workspace.
+namespace dspark {
+namespace {
+__global__ __launch_bounds__(256) void zero_words_kernel(u32* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0u;
+}
+
+int zero_counters(void* base, size_t bytes, hipStream_t s, const char* what) {
+  const long words = (long)(bytes / sizeof(u32));
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s,
+                     static_cast<u32*>(base), words);
+  return check_launch(what);
+}
+}  // namespace
+}  // namespace dspark
+
+extern "C" int dspark_qmm_workspace_reset(void* workspace, size_t workspace_bytes, dspark_stream stream) {
+  if (!workspace) return fail(DSPARK_ERR_ARG, "qmm_workspace_reset: null workspace");
+  if (!aligned(workspace, 256)) return fail(DSPARK_ERR_ALIGN, "qmm_workspace_reset: workspace must be 256-byte aligned");
+  const size_t n = workspace_bytes < kCtrRegionBytes ? workspace_bytes : kCtrRegionBytes;
+  if (n < sizeof(int)) return DSPARK_OK;
+  return zero_counters(workspace, n, static_cast<hipStream_t>(stream), "dspark_qmm_workspace_reset");
+}

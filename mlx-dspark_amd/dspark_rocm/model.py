@@ -16,8 +16,9 @@ Two forwards of the same weights live here:
   one q/k/v qmm launch, one q/k-norm + RoPE + cache-write kernel, split-KV attention writing
   o_proj's input rows directly, the o qmm, residual-add + RMSNorm, one fused gate/up/SwiGLU
   qmm launch (packed weights; else a gate/up launch and the SwiGLU kernel), the down qmm; then
-  the final norm, lm_head, device argmax and greedy accept. All buffers are preallocated, so a
-  step can be captured in a hipGraph.
+  the final norm, lm_head, device argmax and greedy accept. All buffers, the qmm and attention
+  workspaces included, are preallocated for up to ``max_rows`` rows and any cache length, so a
+  step can be captured in a hipGraph and replayed after steps at other depths.
 
 :class:`Target` mirrors the reference's ``verify`` / ``rollback`` / ``make_cache`` surface and
 the greedy round (generate.py:1544-1593).
@@ -32,6 +33,7 @@ import torch
 from torch import nn
 
 from . import fast, ops
+from ._lib import load as _lib_load
 from .kv_cache import KVCache
 from .nn import QuantizedLinear
 
@@ -208,15 +210,39 @@ class VerifyEngine:
         self.tt = torch.zeros(max_rows, dtype=torch.int32, device=dev)
         self.draft = torch.zeros(max(max_rows - 1, 1), dtype=torch.int32, device=dev)
         self.n_acc = torch.zeros(1, dtype=torch.int32, device=dev)
+        # The engine's own workspaces, sized once for every launch of a step at up to max_rows
+        # rows and any cache length, so a captured step never sees them move.
+        self.qmm_ws = ops.new_qmm_workspace(dev, self._qmm_workspace_need())
+        self.attn_ws = torch.empty(max(ops.attention_workspace_bound(1, hq, hk, d, max_rows), 16), dtype=torch.uint8,
+                                   device=dev)
+
+    def _qmm_workspace_need(self) -> int:
+        a, m, M = self.args, self.model, self.max_rows
+        need = []
+        for layer in m.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            groups = [[at.q_proj, at.k_proj, at.v_proj], [at.o_proj], [mlp.down_proj]]
+            pair = self._swiglu.get(id(mlp))
+            if pair is not None:
+                need.append(int(_lib_load().dspark_qmm_swiglu_packed_workspace(pair.n, pair.k, M, pair.bits, 64)))
+            else:
+                groups.append([mlp.gate_proj, mlp.up_proj])
+            for mods in groups:
+                k = mods[0].weight.shape[1] * 32 // mods[0].bits
+                need.append(ops.qmm_launch_workspace_bytes(M, k, [mod.weight.shape[0] for mod in mods], mods[0].bits))
+        lm = m.lm_head
+        need.append(ops.qmm_launch_workspace_bytes(M, a.hidden_size, [lm.weight.shape[0]], lm.bits))
+        return max(need)
 
     def _qmm(self, x: torch.Tensor, mods, outs) -> None:
         """One launch of ``x @ W^T`` for the modules ``mods`` (same K and bits) into ``outs``."""
         packs = [self._packed.get(id(mod)) for mod in mods]
         if all(p is not None for p in packs):
-            ops.quantized_matmul_packed_multi([x], packs, outs=outs)
+            ops.quantized_matmul_packed_multi([x], packs, outs=outs, workspace=self.qmm_ws)
         else:
             ops.quantized_matmul_multi([x], [mod.weight for mod in mods], [mod.scales for mod in mods],
-                                       [mod.biases for mod in mods], bits=mods[0].bits, outs=outs)
+                                       [mod.biases for mod in mods], bits=mods[0].bits, outs=outs,
+                                       workspace=self.qmm_ws)
 
     def step(self, M: int, cache: list[KVCache], pos0: int, *, accept: bool = False) -> torch.Tensor:
         """Run the forward over ``self.ids[:M]`` at cache positions pos0..pos0+M-1 (caches
@@ -243,12 +269,13 @@ class VerifyEngine:
                                 k_cache=c.keys[0], v_cache=c.values[0])
             kv, vv = c.keys[:, :, :L], c.values[:, :, :L]
             att = self.att[:M]
-            ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1)
+            ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1,
+                                      workspace=self.attn_ws)
             self._qmm(att, [at.o_proj], [r])
             ops.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
             pair = self._swiglu.get(id(mlp))
             if pair is not None:
-                ops.quantized_swiglu_packed(y, pair, out=self.hm[:M])
+                ops.quantized_swiglu_packed(y, pair, out=self.hm[:M], workspace=self.qmm_ws)
             else:
                 self._qmm(y, [mlp.gate_proj, mlp.up_proj], [self.g[:M], self.u[:M]])
                 ops.swiglu(self.g[:M], self.u[:M], out=self.hm[:M])

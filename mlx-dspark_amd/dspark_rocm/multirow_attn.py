@@ -25,9 +25,9 @@ from dataclasses import dataclass
 
 import torch
 
-from . import _lib, fast, ops
+from . import _lib, _scope, fast, gate, ops
 
-_ORIG_SDPA = fast.STOCK
+_STOCK = fast.STOCK
 
 MAX_D = 128
 HEAD_DIMS = ops.ATTN_HEAD_DIMS
@@ -73,177 +73,186 @@ class MultirowConfig:
     windows: tuple[Window, ...] = ()
 
     def window(self, hq: int, hk: int, d: int) -> Window | None:
-        for w in self.windows:
-            if w.hq == hq and w.hk == hk and w.d == d:
-                return w
-        return None
+        return next((w for w in self.windows if (w.hq, w.hk, w.d) == (hq, hk, d)), None)
 
 
-def eligible(q, k, v, mask, sinks, cfg: MultirowConfig) -> bool:
-    """Structural + gate check (multirow_attn.py:288-312), on GPU tensors."""
-    return eligible_shape(q, k, v, mask, sinks, cfg) and q.is_cuda and k.is_cuda and v.is_cuda
+def why_not(q, k, v, mask, sinks, cfg: MultirowConfig) -> str | None:
+    """The first reason the kernel cannot serve this call, or None when it can (device aside).
+
+    The conditions are the reference's gate (multirow_attn.py:288-312) plus what torch lets
+    us check that mlx does not expose: K/V must be contiguous along head_dim (any batch, head
+    and sequence strides are fine, e.g. a cache view sliced along the sequence)."""
+    if sinks is not None:
+        return "sinks"
+    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
+        return "mask"
+    if not (q.dim() == k.dim() == v.dim() == 4):
+        return "rank"
+    B, Hq, q_len, D = q.shape
+    Hk, L = k.shape[1], k.shape[2]
+    w = cfg.window(Hq, Hk, D)
+    if w is None:
+        return "unmeasured shape"
+    if not w.min_q <= q_len <= min(w.max_q, L):
+        return "q_len outside the window"
+    if L < max(w.min_kv, 16):
+        return "kv_len below the window"
+    if not (q.dtype in _DTYPES and k.dtype == v.dtype == q.dtype):
+        return "dtype"
+    if D not in HEAD_DIMS or k.shape[-1] != D or v.shape[-1] != D:
+        return "head_dim"
+    if Hk == 0 or Hq % Hk or tuple(v.shape[:3]) != (B, Hk, L) or k.shape[0] != B:
+        return "heads"
+    if (Hq // Hk) * q_len > MAX_ROWS:
+        return "rows"
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        return "head_dim stride"
+    return None
 
 
 def eligible_shape(q, k, v, mask, sinks, cfg: MultirowConfig) -> bool:
-    """No sinks; mask None or "causal"; 4-D bf16 tensors of a measured shape; K/V/Q head dims
-    equal and supported; whole GQA groups; q_len and the KV length inside the shape's window;
-    K/V contiguous along head_dim (checked here — torch exposes strides)."""
-    if sinks is not None or q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-        return False
-    if not (mask is None or (isinstance(mask, str) and mask == "causal")):
-        return False
-    B, Hq, qL, D = q.shape
-    Hk, L = k.shape[1], k.shape[2]
-    w = cfg.window(Hq, Hk, D)
-    if w is None or not (w.min_q <= qL <= w.max_q and qL <= L) or max(w.min_kv, 16) > L:
-        return False
-    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
-        return False
-    if k.shape[-1] != D or v.shape[-1] != D or D not in HEAD_DIMS or v.shape[2] != L:
-        return False
-    if Hk == 0 or Hq % Hk or v.shape[1] != Hk or k.shape[0] != B or v.shape[0] != B:
-        return False
-    return not ((Hq // Hk) * qL > MAX_ROWS or k.stride(-1) != 1 or v.stride(-1) != 1)
+    """Everything :func:`eligible` checks except the device."""
+    return why_not(q, k, v, mask, sinks, cfg) is None
 
 
-_ACTIVE: MultirowConfig | None = None
-_PREV = None
-_TREE: tuple | None = None
+def eligible(q, k, v, mask, sinks, cfg: MultirowConfig) -> bool:
+    """Structural + window check on GPU tensors (multirow_attn.py:288-312)."""
+    return q.is_cuda and k.is_cuda and v.is_cuda and eligible_shape(q, k, v, mask, sinks, cfg)
+
+
+# Scope state: the active config, what the patch falls through to, the registered tree mask.
+_config = _scope.Slot()
+_fallthrough = _scope.Slot()
+_tree = _scope.Slot()
+
+
+def current_tree():
+    """``(mask, anc_bits)`` registered by the innermost :func:`tree_mask`, or None."""
+    return _tree.value
 
 
 @contextlib.contextmanager
 def tree_mask(mask, anc_bits: torch.Tensor):
     """Declare ``mask`` (the exact object a tree verify passes) as a tree-verify mask whose
-    visibility over the last W keys is ``anc_bits`` (uint32 per row). Identity-matched."""
-    global _TREE
-    prev = _TREE
-    _TREE = (mask, anc_bits)
-    try:
+    visibility over the last W keys is ``anc_bits`` (uint32 per row). Calls carrying that
+    object take the kernel's ancestry variant; the match is by identity (multirow_attn.py:319-335)."""
+    with _tree.holding((mask, anc_bits)):
         yield
-    finally:
-        _TREE = prev
+
+
+def _route(q, k, v, scale, mask, sinks, cfg):
+    """The kernel's answer for this call, or None when it does not serve it."""
+    tree = _tree.value
+    if tree is not None and mask is tree[0]:
+        if q.dim() == 4 and q.shape[2] <= 32 and eligible(q, k, v, None, sinks, cfg):
+            return multirow_sdpa(q, k, v, scale=scale, causal=False, tree_anc=tree[1])
+        return None
+    if eligible(q, k, v, mask, sinks, cfg):
+        return multirow_sdpa(q, k, v, scale=scale, causal=mask == "causal" and q.shape[2] > 1)
+    return None
 
 
 def _patched_call(q, k, v, *, scale, mask=None, sinks=None, **kw):
-    cfg = _ACTIVE
-    if cfg is not None and not kw:
-        tree = _TREE
-        if (tree is not None and mask is tree[0] and q.dim() == 4 and q.shape[2] <= 32
-                and eligible(q, k, v, None, sinks, cfg)):
-            return multirow_sdpa(q, k, v, scale=scale, causal=False, tree_anc=tree[1])
-        if eligible(q, k, v, mask, sinks, cfg):
-            return multirow_sdpa(q, k, v, scale=scale, causal=isinstance(mask, str) and q.shape[2] > 1)
-    prev = _PREV or _ORIG_SDPA
-    return prev(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
+    cfg = _config.value
+    out = _route(q, k, v, scale, mask, sinks, cfg) if cfg is not None and not kw else None
+    if out is not None:
+        return out
+    below = _fallthrough.value or _STOCK
+    return below(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
 
 
 @contextlib.contextmanager
 def multirow_attention(cfg: MultirowConfig | None):
     """Route eligible ``fast.scaled_dot_product_attention`` calls through the kernel while
-    active; everything else falls through to what was installed before. No-op when ``cfg``
-    is None or the patch is already installed."""
-    global _ACTIVE, _PREV
-    if cfg is None or fast.scaled_dot_product_attention is _patched_call:
+    active; every other call goes to whatever was installed before (the split scope, then the
+    stock path). No-op when ``cfg`` is None or the patch is already installed."""
+    if cfg is None or active():
         yield
         return
-    prev = fast.scaled_dot_product_attention
-    prev_cfg, prev_prev = _ACTIVE, _PREV
-    _ACTIVE, _PREV = cfg, prev
-    fast.scaled_dot_product_attention = _patched_call
-    try:
+    below = fast.scaled_dot_product_attention
+    with _config.holding(cfg), _fallthrough.holding(below), \
+            _scope.replaced(fast, "scaled_dot_product_attention", _patched_call):
         yield
-    finally:
-        fast.scaled_dot_product_attention = prev
-        _ACTIVE, _PREV = prev_cfg, prev_prev
 
 
 def active() -> bool:
     return fast.scaled_dot_product_attention is _patched_call
 
 
-# ---- measurement (multirow_attn.py:391-488) ------------------------------------------
+# ---- measurement (the reference's gate: multirow_attn.py:391-488) --------------------
 
 PROBE_Q = (2, 4, 6, 8, 12, 16)
 PROBE_KV = (1024, 4096, 16384)
 WIN = 1.05
 
 
-def _chain_ms(fn, q0, kvs, iters: int = 4) -> float:
-    """ms per call over a DEPENDENT chain (each output is the next query) across rotated KV sets."""
-    import time
-
-    def run():
-        q = q0
-        for _ in range(iters):
-            for kk, vv in kvs:
-                q = fn(q, kk, vv)
-        return q
-
-    run()
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    run()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t) * 1e3 / (iters * len(kvs))
+def _window_from_wins(wins: dict[int, set[int]], probe_q, probe_kv) -> dict | None:
+    """The served window from the set of winning q at each probed kv length: ``max_q`` ends
+    the longest run of winning probe q (from the smallest) at the deepest kv; ``min_kv`` is
+    the shortest kv from which every deeper probe also wins that whole run."""
+    deepest = wins.get(probe_kv[-1], set())
+    run = []
+    for ql in probe_q:
+        if ql not in deepest:
+            break
+        run.append(ql)
+    if not run:
+        return None
+    min_kv = probe_kv[-1]
+    for kv in sorted(probe_kv, reverse=True):
+        if not set(run) <= wins.get(kv, set()):
+            break
+        min_kv = kv
+    return {"min_q": probe_q[0], "max_q": run[-1], "min_kv": min_kv}
 
 
 def measure_window(hq: int, hk: int, d: int, *, dtype=torch.bfloat16, device="cuda", verbose: bool = False,
                    probe_q=PROBE_Q, probe_kv=PROBE_KV) -> tuple[dict | None, dict]:
-    """Race the kernel against the stock path on this GPU for shape (hq, hk, d) and return
-    ``(window, report)``. Numerics at every probe against an fp32 reference: the kernel's max
-    |d| must stay within 2x the stock path's + 2e-3, or the shape is refused. ``max_q`` is the
-    widest probed q such that every probed q <= it wins by > 5% at the deepest KV; ``min_kv``
-    the shortest probed KV from which that range wins at every deeper probe."""
+    """Race the kernel against the stock path for shape (hq, hk, d) on this GPU; returns
+    ``(window, report)``. At every probe (q_len, kv_len) the kernel's max |d| from an fp32
+    reference must stay within twice the stock path's plus 2e-3, or the shape is refused; the
+    kernel wins a probe when the stock path takes more than ``WIN`` times as long (HIP-event
+    chains over three KV sets). ``window`` is None when nothing wins or the kernel cannot run."""
     if d not in HEAD_DIMS or hk == 0 or hq % hk or dtype not in _DTYPES:
         return None, {"reason": "shape"}
-    scale = 1.0 / math.sqrt(d)
+    scale = d ** -0.5
     report: dict = {"shape": f"{hq}x{hk}x{d}", "points": {}}
-    wins_at: dict[int, list[int]] = {}
-    g = torch.Generator(device=device)
-    g.manual_seed(0)
+    wins: dict[int, set[int]] = {}
+    gen = torch.Generator(device=device)
+    gen.manual_seed(0)
+
+    def rand(*shape):
+        return torch.randn(shape, generator=gen, device=device).to(dtype)
+
     try:
         for kv in probe_kv:
-            kvs = [(torch.randn((1, hk, kv, d), generator=g, device=device).to(dtype),
-                    torch.randn((1, hk, kv, d), generator=g, device=device).to(dtype)) for _ in range(3)]
-            ok = []
+            sets = [(rand(1, hk, kv, d), rand(1, hk, kv, d)) for _ in range(3)]
+            wins[kv] = set()
             for ql in probe_q:
                 if (hq // hk) * ql > MAX_ROWS:
                     report["points"][f"q{ql}@{kv}"] = "unavailable"
                     break
-                q = torch.randn((1, hq, ql, d), generator=g, device=device).to(dtype)
-                k0, v0 = kvs[0]
-                ref = _ORIG_SDPA(q.float(), k0.float(), v0.float(), scale=scale, mask="causal")
-                o_m = multirow_sdpa(q, k0, v0, scale=scale, causal=True)
-                e_m = float((o_m.float() - ref).abs().max())
-                o_x = _ORIG_SDPA(q, k0, v0, scale=scale, mask="causal")
-                e_x = float((o_x.float() - ref).abs().max())
-                if math.isnan(e_m) or e_m > 2.0 * e_x + 2e-3:
-                    report["reason"] = f"numerics q{ql} kv{kv}: {e_m:.4g} vs stock {e_x:.4g}"
+                q = rand(1, hq, ql, d)
+                kk, vv = sets[0]
+                exact = _STOCK(q.float(), kk.float(), vv.float(), scale=scale, mask="causal")
+                e_kernel = gate.max_abs_diff(multirow_sdpa(q, kk, vv, scale=scale, causal=True), exact)
+                e_stock = gate.max_abs_diff(_STOCK(q, kk, vv, scale=scale, mask="causal"), exact)
+                if not e_kernel <= 2.0 * e_stock + 2e-3:
+                    report["reason"] = f"numerics q{ql} kv{kv}: {e_kernel:.4g} vs stock {e_stock:.4g}"
                     return None, report
-                t_x = _chain_ms(lambda qq, kk, vv: _ORIG_SDPA(qq, kk, vv, scale=scale, mask="causal"), q, kvs)
-                t_m = _chain_ms(lambda qq, kk, vv: multirow_sdpa(qq, kk, vv, scale=scale, causal=True), q, kvs)
-                report["points"][f"q{ql}@{kv}"] = round(t_x / t_m, 2)
-                if t_x > WIN * t_m:
-                    ok.append(ql)
-            wins_at[kv] = ok
-            del kvs
+                ratio = gate.speedup(
+                    [lambda a=a, b=b: _STOCK(q, a, b, scale=scale, mask="causal") for a, b in sets],
+                    [lambda a=a, b=b: multirow_sdpa(q, a, b, scale=scale, causal=True) for a, b in sets])
+                report["points"][f"q{ql}@{kv}"] = round(ratio, 2)
+                if ratio > WIN:
+                    wins[kv].add(ql)
+            del sets
     except Exception as e:  # noqa: BLE001 - a kernel that will not run here is simply off
         report["reason"] = f"kernel unavailable: {type(e).__name__}: {e}"
         return None, report
-    deep = wins_at[probe_kv[-1]]
-    max_q = 0
-    for ql in probe_q:
-        if ql not in deep:
-            break
-        max_q = ql
-    if not max_q:
+    window = _window_from_wins(wins, tuple(probe_q), tuple(probe_kv))
+    if window is None:
         report["reason"] = "no win on this GPU"
-        return None, report
-    qs = [ql for ql in probe_q if ql <= max_q]
-    min_kv = probe_kv[-1]
-    for kv in reversed(probe_kv):
-        if all(ql in wins_at[kv] for ql in qs):
-            min_kv = kv
-        else:
-            break
-    return {"min_q": probe_q[0], "max_q": max_q, "min_kv": min_kv}, report
+    if verbose:
+        print(f"  multirow attention {report['shape']}: {window} {report['points']}", flush=True)
+    return window, report

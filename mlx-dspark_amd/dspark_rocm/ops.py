@@ -91,7 +91,7 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
 
 
 def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = GROUP, bits: int = 4,
-                           outs=None) -> list[torch.Tensor]:
+                           outs=None, workspace: torch.Tensor | None = None) -> list[torch.Tensor]:
     """Several ``quantized_matmul`` with the same M, K and bits in ONE launch (q/k/v; gate/up).
     Bitwise equal to separate calls."""
     cnt = len(w_list)
@@ -123,7 +123,7 @@ def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = 
         probs[i] = _lib.QmmProblem(_ptr(x2), x2.stride(0), _ptr(w), _ptr(s), _ptr(b), _ptr(y), y.stride(0), n, k)
         results.append(y.reshape(*x.shape[:-1], n))
     nbytes = _lib.load().dspark_qmm_affine_multi_workspace(probs, cnt, m, bits, group_size)
-    ws = qmm_workspace(x_list[0].device, nbytes)
+    ws = _pick(workspace, x_list[0].device, nbytes, qmm=True)
     _lib.call("dspark_qmm_affine_multi", probs, cnt, m, bits, group_size, _ptr(ws),
               0 if ws is None else ws.numel(), _stream(x_list[0]))
     return results
@@ -164,7 +164,8 @@ def qmm_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, bit
     return PackedQmm(buf, n, k, bits)
 
 
-def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROUP, outs=None) -> list[torch.Tensor]:
+def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROUP, outs=None,
+                                  workspace: torch.Tensor | None = None) -> list[torch.Tensor]:
     """``quantized_matmul_multi`` over packed matrices (one launch, same M, K and bits)."""
     cnt = len(packed_list)
     if not 1 <= cnt <= _lib.MAX_QMM_PROBLEMS:
@@ -195,7 +196,7 @@ def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROU
         probs[i] = _lib.QmmPackedProblem(_ptr(x2), x2.stride(0), _ptr(pq.buf), _ptr(y), y.stride(0), pq.n, k)
         results.append(y.reshape(*x.shape[:-1], pq.n))
     nbytes = _lib.load().dspark_qmm_packed_multi_workspace(probs, cnt, m, bits, group_size)
-    ws = qmm_workspace(x_list[0].device, nbytes)
+    ws = _pick(workspace, x_list[0].device, nbytes, qmm=True)
     _lib.call("dspark_qmm_packed_multi", probs, cnt, m, bits, group_size, _ptr(ws),
               0 if ws is None else ws.numel(), _stream(x_list[0]))
     return results
@@ -237,7 +238,7 @@ def qmm_pack_swiglu(gate, up, *, bits: int, group_size: int = GROUP) -> PackedSw
 
 
 def quantized_swiglu_packed(x: torch.Tensor, pair: PackedSwiGLU, *, group_size: int = GROUP,
-                            out: torch.Tensor | None = None) -> torch.Tensor:
+                            out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """``silu(x W_gate^T) * (x W_up^T)`` with mlx's bf16 rounding, in one launch -> ``[.., N]``."""
     _require_cuda(x, pair.buf)
     _require_bf16("x", x)
@@ -251,7 +252,7 @@ def quantized_swiglu_packed(x: torch.Tensor, pair: PackedSwiGLU, *, group_size: 
     h = out if out is not None else torch.empty((m, pair.n), dtype=torch.bfloat16, device=x.device)
     lib = _lib.load()
     nbytes = lib.dspark_qmm_swiglu_packed_workspace(pair.n, k, m, pair.bits, group_size)
-    ws = qmm_workspace(x.device, nbytes)
+    ws = _pick(workspace, x.device, nbytes, qmm=True)
     _lib.call("dspark_qmm_swiglu_packed", _ptr(x2), x2.stride(0), _ptr(pair.buf), _ptr(h), h.stride(0), pair.n, k, m,
               pair.bits, group_size, _ptr(ws), 0 if ws is None else ws.numel(), _stream(x))
     return h.reshape(*x.shape[:-1], pair.n)
@@ -264,41 +265,91 @@ def qmm_supported(m: int, k: int, n: int, bits: int, group_size: int = GROUP) ->
 # ---------------------------------------------------------------------------- workspaces
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_qmm_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Buffers a larger request superseded. They are never freed: a HIP graph captured earlier may
+# still hold their addresses, and freeing one would let the caching allocator hand that memory
+# to another tensor which the next replay then overwrites.
+_retired: list[torch.Tensor] = []
+
+
+def _stream_key(device) -> tuple[torch.device, tuple[int, int]]:
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return dev, (idx, torch.cuda.current_stream(dev).cuda_stream)
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A per-(device, stream) scratch buffer reused across calls (stream-ordered reuse is safe;
-    two streams never share one). Grows, never shrinks."""
+    two streams never share one). Grows by replacement; a replaced buffer stays allocated."""
     if nbytes <= 0:
         return None
-    dev = torch.device(device)
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(dev).cuda_stream)
+    dev, key = _stream_key(device)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _retired.append(buf)
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _workspaces[key] = buf
     return buf
 
 
-_qmm_workspaces: dict[tuple[int, int], torch.Tensor] = {}
-
-
 def qmm_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     """The qmm workspace of (device, current stream): zero-filled when allocated (its arrival
     counters must start at zero; every qmm call leaves them zero). Kept apart from the other
-    scratch buffers, which hold arbitrary data between calls."""
+    scratch buffers, which hold arbitrary data between calls. A replaced buffer stays
+    allocated, as for :func:`workspace`."""
     if nbytes <= 0:
         return None
-    dev = torch.device(device)
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(dev).cuda_stream)
+    dev, key = _stream_key(device)
     buf = _qmm_workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        # a replaced buffer is only reused by torch's allocator after this stream's pending work
+        if buf is not None:
+            _retired.append(buf)
         buf = torch.zeros(max(nbytes, 4 << 20), dtype=torch.uint8, device=dev)
         _qmm_workspaces[key] = buf
     return buf
+
+
+def new_qmm_workspace(device, nbytes: int) -> torch.Tensor | None:
+    """A caller-owned qmm workspace of at least ``nbytes`` (zeroed: the arrival counters must
+    start at zero), e.g. for a graph-captured engine that must not share the per-stream one."""
+    if nbytes <= 0:
+        return None
+    return torch.zeros(max(int(nbytes), 256 << 10), dtype=torch.uint8, device=device)
+
+
+def qmm_launch_workspace_bytes(m: int, k: int, ns, bits: int, group_size: int = GROUP) -> int:
+    """Workspace bytes of one qmm launch over matrices [n, k] for n in ``ns`` with ``m`` rows
+    (the reference and the packed layout plan alike). Host query only: the problem pointers it
+    passes are placeholders the library does not dereference."""
+    ns = list(ns)
+    probs = (_lib.QmmProblem * len(ns))()
+    for i, n in enumerate(ns):
+        probs[i] = _lib.QmmProblem(256, k, 256, 256, 256, 256, n, n, k)
+    return int(_lib.load().dspark_qmm_affine_multi_workspace(probs, len(ns), m, bits, group_size))
+
+
+def attention_workspace_bound(batch: int, hq: int, hk: int, d: int, max_rows: int) -> int:
+    """The most workspace bytes verify attention needs for up to ``max_rows`` query rows at any
+    cache length: the plan caps its key blocks by the grid size, not by the length."""
+    lib = _lib.load()
+    return max(int(lib.dspark_verify_attention_workspace(batch, hq, hk, m, d, 1 << 29)) for m in range(1, max_rows + 1))
+
+
+def qmm_workspace_reset(ws: torch.Tensor) -> None:
+    """Zero the split-K arrival counters of a qmm workspace on the current stream (a fill
+    kernel, so it may be captured): restores the state every completed qmm call leaves."""
+    _require_cuda(ws)
+    _lib.call("dspark_qmm_workspace_reset", _ptr(ws), ws.numel(), _stream(ws))
+
+
+def _pick(ws: torch.Tensor | None, device, nbytes: int, qmm: bool):
+    """The caller's workspace when given (checked for size), else the per-stream one."""
+    if ws is None:
+        return qmm_workspace(device, nbytes) if qmm else workspace(device, nbytes)
+    if ws.numel() < nbytes:
+        raise ValueError(f"workspace of {ws.numel()} bytes < {nbytes} needed")
+    return ws
 
 
 # ---------------------------------------------------------------------------- verify attention
@@ -425,7 +476,8 @@ def moe_switch_glu(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: 
 
 
 def verify_attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, out_strides, *,
-                          scale: float, causal: bool = True, tree_anc: torch.Tensor | None = None) -> torch.Tensor:
+                          scale: float, causal: bool = True, tree_anc: torch.Tensor | None = None,
+                          workspace: torch.Tensor | None = None) -> torch.Tensor:
     """:func:`verify_attention` writing through element strides ``out_strides`` = (batch, query
     head, position) of ``out`` (head_dim contiguous), e.g. [B, Mq, Hq*D] rows for o_proj."""
     _require_cuda(q, k, v, out)
@@ -433,7 +485,7 @@ def verify_attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out
     Hk, L = k.shape[1], k.shape[2]
     q = q.contiguous()
     nbytes = _lib.load().dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
-    ws = workspace(q.device, nbytes)
+    ws = _pick(workspace, q.device, nbytes, qmm=False)
     anc = None if tree_anc is None else tree_anc.to(device=q.device, dtype=torch.int32).contiguous()
     os_ = (ctypes.c_int64 * 3)(*[int(s) for s in out_strides])
     _lib.call("dspark_verify_attention_strided", _ptr(q), B, Hq, mq, D, _ptr(k), _ptr(v), _i64x3(k), _i64x3(v), Hk, L,

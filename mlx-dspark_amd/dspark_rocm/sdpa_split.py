@@ -1,33 +1,37 @@
-"""Split a wide-verify SDPA into narrow sub-calls (the reference's fallback path).
+"""Row-split attention: a wide verify SDPA computed as several narrow sub-calls.
 
-Mirrors sdpa_split.py: each query row's attention is independent, so computing the q_len rows
-in balanced <= ``max_chunk``-row sub-calls and concatenating equals one call per row up to
-reduction order (sdpa_split.py:9-14). For the string "causal" mask, chunk rows [off, off+p)
-are the last rows of a shorter problem: they attend ``k[..., :kv_len - q_len + off + p]``
-under the same "causal" rule (sdpa_split.py:84-87); array masks are sliced per row.
+The reference uses this to step around a slow multi-row path of its stock attention
+(sdpa_split.py:1-23, entry points :38-134). It is exact per row because every query row's
+output depends only on that row and the keys it may see (sdpa_split.py:9-14), so cutting the
+q_len rows into blocks and concatenating the block outputs changes only the reduction order.
 
-The scope ``sdpa_split(cfg)`` patches :func:`dspark_rocm.fast.scaled_dot_product_attention`
-(the reference patches ``mx.fast.scaled_dot_product_attention``) and restores it on exit;
-:mod:`.multirow_attn` installs over it and falls through to it.
+Rows [a, b) of a ``"causal"`` call are the last ``b - a`` rows of a problem whose keys end at
+``kv_len - q_len + b``: their sub-call keeps the "causal" string over that key prefix
+(sdpa_split.py:84-87). An array mask of shape [..., q_len, kv_len] is cut to the block's rows;
+one of shape [..., 1, kv_len] is shared by every block.
+
+``sdpa_split(cfg)`` replaces :func:`dspark_rocm.fast.scaled_dot_product_attention` while
+active. Blocks always call the stock function captured at import, never the replaced entry
+point, so a split sub-call does not come back through any scope.
 """
 
 from __future__ import annotations
 
 import contextlib
-import math
 from dataclasses import dataclass
+from itertools import accumulate
 
 import torch
 
-from . import fast
+from . import _scope, fast
 
-_ORIG_SDPA = fast.scaled_dot_product_attention
+_STOCK = fast.scaled_dot_product_attention
 
 
 @dataclass(frozen=True)
 class SplitConfig:
-    """Split fires iff ``min_q <= q_len <= max_q`` and ``kv_len >= min_kv``; ``max_chunk``
-    bounds each sub-call's q_len."""
+    """The split fires iff ``min_q <= q_len <= max_q`` and ``kv_len >= min_kv``; every
+    sub-call then has at most ``max_chunk`` rows."""
     min_q: int = 6
     max_q: int = 15
     min_kv: int = 4096
@@ -35,77 +39,62 @@ class SplitConfig:
 
 
 def _partition(q_len: int, max_chunk: int) -> list[int]:
-    """Balanced split of ``q_len`` into ceil(q_len / max_chunk) chunks, larger chunks first."""
-    n = max(1, math.ceil(q_len / max_chunk))
-    base, rem = divmod(q_len, n)
-    return [base + 1] * rem + [base] * (n - rem)
+    """Block sizes: the fewest blocks of at most ``max_chunk`` rows, as even as possible,
+    larger blocks first. Uses sum_{i<n} floor((q + i) / n) = q."""
+    n = max(1, -(-q_len // max_chunk))
+    return [(q_len + i) // n for i in range(n - 1, -1, -1)]
+
+
+def _fires(cfg: SplitConfig, q_len: int, kv_len: int) -> bool:
+    return cfg.min_q <= q_len <= cfg.max_q and kv_len >= cfg.min_kv
 
 
 def split_sdpa(q, k, v, *, scale, mask=None, sinks=None, cfg: SplitConfig, _orig=None, **kw):
-    """``scaled_dot_product_attention`` computed in row chunks when the gate fires; a single
-    call (verbatim) otherwise."""
-    orig = _orig or _ORIG_SDPA
-    q_len = q.shape[-2]
-    kv_len = k.shape[-2]
-    if not (cfg.min_q <= q_len <= cfg.max_q and kv_len >= cfg.min_kv):
-        return orig(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
-    is_str_mask = isinstance(mask, str)
-    is_arr_mask = isinstance(mask, torch.Tensor)
-    if is_arr_mask:
-        mq = mask.shape[-2] if mask.dim() >= 2 else 1
-        if mq not in (1, q_len):
-            return orig(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
-    outs = []
-    off = 0
-    for p in _partition(q_len, cfg.max_chunk):
-        qc = q[..., off:off + p, :]
-        if mask is None:
-            oc = orig(qc, k, v, scale=scale, mask=None, sinks=sinks, **kw)
-        elif is_str_mask:
-            end = kv_len - q_len + off + p
-            oc = orig(qc, k[..., :end, :], v[..., :end, :], scale=scale, mask=mask, sinks=sinks, **kw)
-        else:
-            mc = mask if mask.shape[-2] == 1 else mask[..., off:off + p, :]
-            oc = orig(qc, k, v, scale=scale, mask=mc, sinks=sinks, **kw)
-        outs.append(oc)
-        off += p
-    return torch.cat(outs, dim=-2)
+    """``scaled_dot_product_attention(q, k, v, ...)`` computed in row blocks when ``cfg``
+    fires for this (q_len, kv_len); one unchanged call otherwise, or when an array mask's row
+    dimension is neither 1 nor q_len."""
+    sdpa = _orig or _STOCK
+    q_len, kv_len = q.shape[-2], k.shape[-2]
+    array_mask = isinstance(mask, torch.Tensor)
+    mask_rows = (mask.shape[-2] if mask.dim() >= 2 else 1) if array_mask else None
+    if not _fires(cfg, q_len, kv_len) or (array_mask and mask_rows not in (1, q_len)):
+        return sdpa(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
+    sizes = _partition(q_len, cfg.max_chunk)
+    ends = list(accumulate(sizes))
+    pieces = []
+    for stop, size in zip(ends, sizes):
+        rows = slice(stop - size, stop)
+        keys, values, block_mask = k, v, mask
+        if isinstance(mask, str):
+            visible = kv_len - q_len + stop
+            keys, values = k[..., :visible, :], v[..., :visible, :]
+        elif array_mask and mask_rows != 1:
+            block_mask = mask[..., rows, :]
+        pieces.append(sdpa(q[..., rows, :], keys, values, scale=scale, mask=block_mask, sinks=sinks, **kw))
+    return torch.cat(pieces, dim=-2)
 
 
-_ACTIVE: SplitConfig | None = None
+_config = _scope.Slot()
 
 
 def _patched_call(q, k, v, *, scale, mask=None, sinks=None, **kw):
-    cfg = _ACTIVE
+    cfg = _config.value
     if cfg is None:
-        return _ORIG_SDPA(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
-    return split_sdpa(q, k, v, scale=scale, mask=mask, sinks=sinks, cfg=cfg, _orig=_ORIG_SDPA, **kw)
+        return _STOCK(q, k, v, scale=scale, mask=mask, sinks=sinks, **kw)
+    return split_sdpa(q, k, v, scale=scale, mask=mask, sinks=sinks, cfg=cfg, _orig=_STOCK, **kw)
 
 
 @contextlib.contextmanager
 def sdpa_split(cfg: SplitConfig | None):
-    """Route ``fast.scaled_dot_product_attention`` through the split while active. No-op when
-    ``cfg`` is None or the split is already installed."""
-    global _ACTIVE
+    """Route ``fast.scaled_dot_product_attention`` through :func:`split_sdpa` while active.
+    A ``None`` config, or a split already installed, makes this scope a no-op."""
     if cfg is None or fast.scaled_dot_product_attention is _patched_call:
         yield
         return
-    prev = fast.scaled_dot_product_attention
-    prev_cfg = _ACTIVE
-    _ACTIVE = cfg
-    fast.scaled_dot_product_attention = _patched_call
-    try:
+    with _config.holding(cfg), _scope.replaced(fast, "scaled_dot_product_attention", _patched_call):
         yield
-    finally:
-        fast.scaled_dot_product_attention = prev
-        _ACTIVE = prev_cfg
 
 
 def patchable() -> bool:
-    """True iff the attention entry point can be replaced (always, on this module)."""
-    try:
-        orig = fast.scaled_dot_product_attention
-        fast.scaled_dot_product_attention = orig
-        return True
-    except (AttributeError, TypeError):
-        return False
+    """Whether the attention entry point accepts a replacement (on this module it always does)."""
+    return _scope.can_replace(fast, "scaled_dot_product_attention")

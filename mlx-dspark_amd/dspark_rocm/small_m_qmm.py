@@ -1,28 +1,30 @@
 """Small-M quantized matmul for the verify window: dispatch, per-shape gate, scoped patch.
 
-Mirrors the reference module (small_m_qmm.py) on torch: inside ``small_m_matmul(ids)`` the
-``QuantizedLinear`` instances whose ``id`` is allowlisted send bf16 forwards with
-``lo <= M <= hi`` rows (M = product of the leading dims) through :mod:`.skinny_qmm`
-(the gfx950 kernel); every other call — unlisted instance, non-bf16 x, rows outside the
-window, scope inactive — runs the module's stock path unchanged (small_m_qmm.py:71-80).
+The reference's entry points (small_m_qmm.py:57-243) on torch modules:
 
-The patch is class-wide on ``QuantizedLinear.forward`` and restores the value it found on
-entry, so it nests with other scopes holding the class (small_m_qmm.py:83-106; reference test
-tests/test_small_m_qmm.py:159-171). :func:`measure_shapes` is the runtime gate
-(small_m_qmm.py:142-230): numerics of the kernel against the stock path at M in
-{lo, 8, 12, hi} (``max|d| <= 0.02 * max(max|ref|, 1)``) and a dependent-chain race over the
-model's own same-shape layers (win >= 1.15x at M = 8 and 12, >= 0.97x at the bottom edge);
-only shapes that pass are returned. Nothing there may raise: a kernel failure disables that
-shape and the stock path stays.
+* ``small_m_matmul(ids)`` replaces ``QuantizedLinear.forward`` class-wide while active. A
+  forward goes to the gfx950 kernel (:mod:`.skinny_qmm`) when the instance's ``id`` is in the
+  allowlist, x is bf16 and its row count (product of the leading dims) lies in the width's
+  ``WINDOW``; every other forward runs the method that was installed on entry, unchanged
+  (small_m_qmm.py:71-80). Exit restores that method, so the scope nests with others holding
+  the class (tests/test_small_m_qmm.py:159-171).
+* ``measure_shapes(*models)`` is the load-time gate (small_m_qmm.py:142-230): per distinct
+  shape, the kernel must agree with the stock path (``max|d| <= 0.02 * max(max|stock|, 1)``
+  at M in {lo, 8, 12, hi}) and win a race over the model's own same-shape layers: 1.15x at
+  M = 8 and 12, and no worse than 0.97x at the bottom of the window when it starts below 6.
+  The race is :func:`dspark_rocm.gate.speedup` (HIP events). A shape whose kernel raises is
+  off; nothing here raises.
 """
 
 from __future__ import annotations
 
 import contextlib
-import time
+import math
+from collections import defaultdict
 
 import torch
 
+from . import _scope, gate
 from . import skinny_qmm as _sk
 from .nn import QuantizedLinear
 
@@ -31,7 +33,8 @@ M8_MIN, M8_MAX = _sk.WINDOW[8]
 M_MIN, M_MAX = M8_MIN, M8_MAX
 
 _orig_call = QuantizedLinear.forward
-_active_ids: frozenset | None = None
+_allow = _scope.Slot()          # frozenset of module ids while a scope is active
+_below = _scope.Slot()          # the forward installed when the scope was entered
 
 
 def _in_features(mod) -> int:
@@ -39,172 +42,142 @@ def _in_features(mod) -> int:
 
 
 def eligible(mod) -> bool:
-    """Can this ``QuantizedLinear``'s shape/format run on the kernel at all?"""
+    """Whether a module's shape and format can run on the kernel at all."""
     return isinstance(mod, QuantizedLinear) and _sk.fits(mod)
 
 
 def shape_key(mod) -> str:
+    """``"{in}x{out}b{bits}"``: modules with one key share a gate verdict."""
     return f"{_in_features(mod)}x{int(mod.weight.shape[0])}b{int(mod.bits)}"
 
 
 def _rows(x) -> int:
-    m = 1
-    for d in x.shape[:-1]:
-        m *= int(d)
-    return m
+    return math.prod(int(d) for d in x.shape[:-1])
 
 
 def serves(mod, x) -> bool:
-    """Would the active scope send this call to the kernel? (allowlisted instance, bf16 x,
-    rows inside the width's window; small_m_qmm.py:71-80)"""
-    if _active_ids is None or id(mod) not in _active_ids or x.dtype != torch.bfloat16:
+    """Would the active scope send this forward to the kernel?"""
+    allow = _allow.value
+    if not allow or id(mod) not in allow or x.dtype != torch.bfloat16:
         return False
     lo, hi = _sk.WINDOW[int(mod.bits)]
     return lo <= _rows(x) <= hi
 
 
 def _mma_call(self, x):
-    if serves(self, x) and x.is_cuda:
+    if x.is_cuda and serves(self, x):
         return _sk.call(self, x, _rows(x))
-    return _orig_call(self, x)
+    return (_below.value or _orig_call)(self, x)
 
 
 @contextlib.contextmanager
 def small_m_matmul(ids: frozenset | None):
-    """Route the allowlisted ``QuantizedLinear`` instances (by ``id``) through the kernel for
-    forwards inside their width's window. ``None``/empty: a no-op scope."""
-    global _active_ids
-    if not ids or QuantizedLinear.forward is _mma_call:
+    """Send the allowlisted ``QuantizedLinear`` instances (by ``id``) to the kernel for
+    forwards inside their width's window. An empty or ``None`` allowlist, or a scope already
+    installed, makes this a no-op."""
+    if not ids or active():
         yield
         return
-    prev = QuantizedLinear.forward
-    _active_ids = frozenset(ids)
-    QuantizedLinear.forward = _mma_call
-    try:
+    with _allow.holding(frozenset(ids)), _below.holding(QuantizedLinear.forward), \
+            _scope.replaced(QuantizedLinear, "forward", _mma_call):
         yield
-    finally:
-        QuantizedLinear.forward = prev
-        _active_ids = None
 
 
 def active() -> bool:
     return QuantizedLinear.forward is _mma_call
 
 
-# ------------------------------------------------------------------ calibration
+# ------------------------------------------------------------------ load-time gate
 
-_CHAIN = 12
+_CHAIN = 12          # calls per timed chain (rotating over the shape's modules)
 _EVALS = 4
 _MIN_GAIN = 1.15
 _EDGE_MIN = 0.97
 _REL_TOL = 0.02
 
 
-def _time_chain(step, x0) -> float:
-    """Seconds per step of a DEPENDENT chain (each step's input depends on the previous output),
-    median of the timed evaluations after a warm-up."""
-    times = []
-    for _ in range(_EVALS):
-        x = x0
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for t in range(_CHAIN):
-            y = step(x, t)
-            x = x0 + (y.float().mean() * 1e-20).to(x0.dtype)
-        torch.cuda.synchronize()
-        times.append((time.perf_counter() - t0) / _CHAIN)
-    rest = sorted(times[1:])
-    return rest[len(rest) // 2]
-
-
 def _kernel_rows(mod, x: torch.Tensor) -> torch.Tensor:
     return _sk.qmm(x, mod.weight, mod.scales, mod.biases, int(mod.bits))
 
 
-def measure_shapes(*models, verbose: bool = False) -> list[str]:
-    """Shape keys whose kernel path is numerically sane and faster than the stock path here."""
-    groups: dict[str, list] = {}
-    for model in models:
-        if model is None:
-            continue
-        for _, mod in model.named_modules():
-            if eligible(mod):
-                groups.setdefault(shape_key(mod), []).append(mod)
-    won: list[str] = []
-    for key, mods in groups.items():
-        try:
-            on = _verdict(key, mods, verbose)
-        except Exception as e:  # noqa: BLE001 - a kernel that will not launch is simply off
-            if verbose:
-                print(f"  small-M qmm: {key} rejected (kernel unavailable: {type(e).__name__}: {e})", flush=True)
-            continue
-        if on:
-            won.append(key)
-    return won
+def _probe_x(K: int, M: int, gen: torch.Generator, device) -> torch.Tensor:
+    return (0.1 * torch.randn((M, K), generator=gen, device=device)).to(torch.bfloat16)
 
 
 def numerics_ok(mod, seed: int = 0) -> bool:
-    """The kernel against the stock path at M in {lo, 8, 12, hi}:
-    ``max|kernel - stock| <= 0.02 * max(max|stock|, 1)`` (small_m_qmm.py:120, :199-205)."""
+    """Kernel vs stock at M in {lo, 8, 12, hi}: ``max|kernel - stock| <= 0.02 * max(max|stock|, 1)``
+    (the module's own bias, if any, is left out of both)."""
     K = _in_features(mod)
     lo, hi = _sk.WINDOW[int(mod.bits)]
-    dev = mod.weight.device
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
+    gen = torch.Generator(device=mod.weight.device)
+    gen.manual_seed(seed)
+    bias = getattr(mod, "bias", None)
     for M in sorted({lo, 8, 12, hi}):
-        x = (torch.randn((M, K), generator=g, device=dev) * 0.1).to(torch.bfloat16)
-        ref = _orig_call(mod, x).float()
-        if getattr(mod, "bias", None) is not None:
-            ref = ref - mod.bias.float()
-        got = _kernel_rows(mod, x).float()
-        diff = (ref - got).abs().max().item()
-        if not diff <= _REL_TOL * max(ref.abs().max().item(), 1.0):
+        x = _probe_x(K, M, gen, mod.weight.device)
+        stock = _orig_call(mod, x).float()
+        if bias is not None:
+            stock = stock - bias.float()
+        scale = max(float(stock.abs().max()), 1.0)
+        if not gate.max_abs_diff(_kernel_rows(mod, x), stock) <= _REL_TOL * scale:
             return False
     return True
 
 
-def _verdict(key: str, mods: list, verbose: bool) -> bool:
-    mod = mods[0]
-    K = _in_features(mod)
-    lo, hi = _sk.WINDOW[int(mod.bits)]
-    dev = mod.weight.device
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    if not numerics_ok(mod):
+def _bars(bits: int) -> list[gate.Bar]:
+    lo = _sk.WINDOW[bits][0]
+    bars = [gate.Bar(8, _MIN_GAIN), gate.Bar(12, _MIN_GAIN)]
+    if lo < 6:
+        bars.append(gate.Bar(lo, _EDGE_MIN))
+    return bars
+
+
+def _race(mods: list, rows: int, gen: torch.Generator) -> float:
+    """Stock / kernel time at ``rows`` rows over chains rotating through ``mods``."""
+    x = _probe_x(_in_features(mods[0]), rows, gen, mods[0].weight.device)
+    seq = [mods[t % len(mods)] for t in range(_CHAIN)]
+    return gate.speedup([lambda m=m: _orig_call(m, x) for m in seq],
+                        [lambda m=m: _kernel_rows(m, x) for m in seq], repeat=_EVALS - 1)
+
+
+def _shape_verdict(key: str, mods: list, verbose: bool) -> bool:
+    if not numerics_ok(mods[0]):
         if verbose:
-            print(f"  small-M qmm: {key} rejected (numerics)", flush=True)
+            print(f"  small-M qmm: {key} off (numerics)", flush=True)
         return False
-
-    def race(M):
-        x = (torch.randn((M, K), generator=g, device=dev) * 0.1).to(torch.bfloat16)
-
-        def q_step(xx, t):
-            return _orig_call(mods[t % len(mods)], xx)
-
-        def k_step(xx, t):
-            return _kernel_rows(mods[t % len(mods)], xx)
-
-        tq = min(_time_chain(q_step, x), _time_chain(q_step, x))
-        tk = min(_time_chain(k_step, x), _time_chain(k_step, x))
-        return tq / tk
-
-    g8, g12 = race(8), race(12)
-    g_lo = race(lo) if lo < 6 else None
-    on = g8 >= _MIN_GAIN and g12 >= _MIN_GAIN and (g_lo is None or g_lo >= _EDGE_MIN)
+    gen = torch.Generator(device=mods[0].weight.device)
+    gen.manual_seed(0)
+    results = [(bar, _race(mods, bar.rows, gen)) for bar in _bars(int(mods[0].bits))]
+    on = all(bar.met(r) for bar, r in results)
     if verbose:
-        edge = f", M={lo} {g_lo:.2f}x" if g_lo is not None else ""
-        print(f"  small-M qmm: {key} M=8 {g8:.2f}x, M=12 {g12:.2f}x{edge} ({'on' if on else 'off'})", flush=True)
+        detail = ", ".join(f"M={bar.rows} {r:.2f}x (>= {bar.min_speedup})" for bar, r in results)
+        print(f"  small-M qmm: {key} {detail}: {'on' if on else 'off'}", flush=True)
     return on
 
 
+def _by_shape(models) -> dict[str, list]:
+    groups: dict[str, list] = defaultdict(list)
+    for model in (m for m in models if m is not None):
+        for mod in model.modules():
+            if eligible(mod):
+                groups[shape_key(mod)].append(mod)
+    return groups
+
+
+def measure_shapes(*models, verbose: bool = False) -> list[str]:
+    """Shape keys whose kernel path agrees with the stock path and wins the race here."""
+    won = []
+    for key, mods in _by_shape(models).items():
+        try:
+            if _shape_verdict(key, mods, verbose):
+                won.append(key)
+        except Exception as e:  # noqa: BLE001 - a kernel that will not launch leaves the shape off
+            if verbose:
+                print(f"  small-M qmm: {key} off (kernel unavailable: {type(e).__name__}: {e})", flush=True)
+    return won
+
+
 def ids_for_shapes(shapes, *models) -> frozenset:
-    """The instance allowlist for :func:`small_m_matmul`, from verified shape keys."""
+    """The instance allowlist for :func:`small_m_matmul`: every eligible module of ``models``
+    whose shape key is in ``shapes``."""
     keys = set(shapes)
-    out = set()
-    for model in models:
-        if model is None:
-            continue
-        for _, mod in model.named_modules():
-            if eligible(mod) and shape_key(mod) in keys:
-                out.add(id(mod))
-    return frozenset(out)
+    return frozenset(id(mod) for key, mods in _by_shape(models).items() if key in keys for mod in mods)

@@ -56,3 +56,4 @@ def test_plan_blocks_scale_with_length():
     assert nb == sorted(nb) and nb[0] >= 1
     # every block covers whole 64-key tiles and the blocks cover the cache
     assert lib.dspark_verify_attention_workspace(1, 32, 8, 16, 128, 64) == 0   # one block: no partials
+

@@ -63,8 +63,48 @@ def test_small_m_leading_dims_and_numerics_gate(dev):
     assert y.shape == (2, 3, 256)
     assert torch.equal(y.reshape(6, 256), sk.qmm(x.reshape(6, 512), mod.weight, mod.scales, mod.biases, 4))
     assert sm.numerics_ok(mod)
-    won = sm.measure_shapes(torch.nn.ModuleList([mod, _ql(dev, 4, 256, 512, 4)]))
-    assert set(won) <= {sm.shape_key(mod)}
+
+
+def test_small_m_gate_verdicts(dev, monkeypatch):
+    """The gate returns a shape exactly when numerics pass and every race bar is met: a race the
+    kernel wins enables the shape, one bar missed disables it, a kernel output that drifts from
+    the stock path disables it whatever the race says."""
+    from dspark_rocm import small_m_qmm as sm
+
+    mods = torch.nn.ModuleList([_ql(dev, 4, 256, 512, 3), _ql(dev, 4, 256, 512, 4), _ql(dev, 8, 128, 512, 5)])
+    key4, key8 = sm.shape_key(mods[0]), sm.shape_key(mods[2])
+    seen = []
+
+    def race(ratio_at):
+        def fake(ms, rows, gen):
+            seen.append((sm.shape_key(ms[0]), rows, len(ms)))
+            return ratio_at(rows)
+        return fake
+
+    monkeypatch.setattr(sm, "_race", race(lambda rows: 2.0))
+    assert sorted(sm.measure_shapes(mods)) == sorted([key4, key8])
+    # both 4-bit modules race together; the window starts at M = 1 < 6, so the edge bar is raced
+    assert (key4, 8, 2) in seen and (key4, 12, 2) in seen and (key4, 1, 2) in seen
+    monkeypatch.setattr(sm, "_race", race(lambda rows: 1.10 if rows == 12 else 2.0))     # M = 12 below 1.15
+    assert sm.measure_shapes(mods) == []
+    monkeypatch.setattr(sm, "_race", race(lambda rows: 0.96 if rows == 1 else 2.0))      # edge below 0.97
+    assert sm.measure_shapes(mods) == []
+    monkeypatch.setattr(sm, "_race", race(lambda rows: 0.97 if rows == 1 else 1.15))     # every bar met exactly
+    assert len(sm.measure_shapes(mods)) == 2
+    monkeypatch.setattr(sm, "_race", race(lambda rows: 2.0))
+    real = sm._kernel_rows
+    monkeypatch.setattr(sm, "_kernel_rows", lambda mod, x: real(mod, x) * 1.05 + 0.5)    # drifted kernel
+    assert sm.measure_shapes(mods) == []
+
+
+def test_small_m_gate_enables_a_real_shape(dev):
+    """The real race on an 8B-shaped projection (4096 x 4096, 8-bit, four layers): the kernel
+    must clear the reference's bars (1.15x at M = 8 and 12, 0.97x at M = 1) against the stock
+    dequantize-and-matmul path on this GPU."""
+    from dspark_rocm import small_m_qmm as sm
+
+    mods = torch.nn.ModuleList([_ql(dev, 8, 4096, 4096, 20 + i) for i in range(4)])
+    assert sm.measure_shapes(mods, verbose=True) == [sm.shape_key(mods[0])]
 
 
 def _kv(dev, hk, L, d, seed, cap_extra=32):

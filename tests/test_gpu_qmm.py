@@ -162,3 +162,25 @@ def test_split_k_workspace_reuse_is_bitwise_stable(dev, bits):
             assert torch.equal(again, first[i]), (rep, i)
     for (xd, wd, sd, bd, host), y in zip(inputs, first):
         _check(from_dev_bf16(y), qmm_ref.qmm_f64(*host, bits), "split-K")
+
+
+def test_workspace_reset_restores_counters(dev):
+    """dspark_qmm_workspace_reset zeroes the arrival counters of a workspace whose counters hold
+    arbitrary values (e.g. after a call that did not complete); the next call is then bitwise the
+    call on a fresh zeroed workspace. Only the reset path runs: no launch sees the stale counters."""
+    import torch
+
+    from dspark_rocm import ops
+
+    x, w, s, b = _problem(61, 16, 4096, 4096, 8)
+    xd, wd, sd, bd = to_dev_bf16(x, dev), to_dev_packed(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+    want = ops.quantized_matmul(xd, wd, sd, bd, bits=8)
+    ws = ops.new_qmm_workspace(dev, 8 << 20)
+    ws[: 256 << 10].fill_(7)                       # stale counters
+    ops.qmm_workspace_reset(ws)
+    torch.cuda.synchronize()
+    assert not ws[: 256 << 10].any()
+    y = torch.empty_like(want)
+    ops.quantized_matmul_multi([xd], [wd], [sd], [bd], bits=8, outs=[y], workspace=ws)
+    assert torch.equal(y, want)
+    assert not ws[: 256 << 10].any()               # and the call leaves them at zero

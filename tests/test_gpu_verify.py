@@ -207,3 +207,47 @@ def test_packed_engine_is_bitwise_the_reference_layout_engine(dev):
         assert torch.equal(la, lb)
         packed.rollback(ca, rej)
         plain.rollback(cb, rej)
+
+
+def test_captured_step_replays_after_deeper_eager_steps(dev):
+    """A verify step captured at a short cache length stays correct when eager steps at a much
+    deeper length (whose attention plan needs more split-KV partials) run on the same stream
+    between replays: the engine's workspaces are sized at construction for any length, so no
+    buffer a graph holds is replaced. Every replay is bitwise the eager result at the short
+    length."""
+    from dspark_rocm.model import Target
+
+    model = tiny_model(dev, seed=10)
+    tgt = Target(model)
+    e = tgt.engine
+    cache = tgt.make_cache(4096 + 64)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    for c in cache:
+        c.keys.normal_(generator=g)
+        c.values.normal_(generator=g)
+    M, short, deep = 16, 600, 4000
+    a = model.args
+    from dspark_rocm import ops
+    assert ops.verify_attention_blocks(1, a.num_attention_heads, a.num_key_value_heads, M, a.head_dim, deep + M) > \
+        ops.verify_attention_blocks(1, a.num_attention_heads, a.num_key_value_heads, M, a.head_dim, short + M) > 1
+    e.ids[:M].copy_(torch.randint(0, a.vocab_size, (M,), generator=g, device=dev))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        e.step(M, cache, short)
+        want = e.logits[:M].clone()
+        e.step(M, cache, short)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        e.step(M, cache, short)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        with torch.cuda.stream(s):
+            e.step(M, cache, deep + 8 * rep)
+            deep_logits = e.logits[:M].clone()
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(e.logits[:M], want), rep
+        assert not torch.equal(deep_logits, want)

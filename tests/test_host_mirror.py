@@ -164,6 +164,7 @@ def test_multirow_eligibility_gate():
     assert not eligible_shape(q.float(), k.float(), v.float(), "causal", None, cfg)  # dtype
     kt = _bf(1, 2, 64, 256).transpose(-1, -2)                            # head_dim not contiguous
     assert not eligible_shape(q, kt, v, "causal", None, cfg)
+    assert not eligible_shape(q, k, v, "bidirectional", None, cfg)                # unknown string mask
     kv_view = _bf(1, 2, 512, 64)[:, :, :256]                              # sequence-sliced view: fine
     assert eligible_shape(q, kv_view, kv_view, "causal", None, cfg)
 
@@ -193,16 +194,30 @@ def test_multirow_scope_restores_on_exception():
     assert fast.scaled_dot_product_attention is stock and not multirow_attn.active()
 
 
+def test_window_from_wins():
+    """The served window: the longest run of winning q (from the smallest probe) at the deepest
+    kv, and the shortest kv from which every deeper probe wins that run."""
+    from dspark_rocm.multirow_attn import _window_from_wins
+
+    q, kv = (2, 4, 6, 8, 12, 16), (1024, 4096, 16384)
+    assert _window_from_wins({16384: {2, 4, 6, 8}, 4096: {2, 4, 6, 8, 12}, 1024: {2, 4}}, q, kv) == \
+        {"min_q": 2, "max_q": 8, "min_kv": 4096}
+    assert _window_from_wins({16384: set(q), 4096: set(q), 1024: set(q)}, q, kv)["min_kv"] == 1024
+    assert _window_from_wins({16384: {4, 6}}, q, kv) is None            # q = 2 lost: no run
+    assert _window_from_wins({16384: {2, 6}, 4096: {2}}, q, kv) == {"min_q": 2, "max_q": 2, "min_kv": 4096}
+    assert _window_from_wins({16384: {2}, 4096: set(), 1024: {2}}, q, kv)["min_kv"] == 16384
+
+
 def test_tree_mask_scope_is_identity_matched_and_restored():
     from dspark_rocm import multirow_attn
 
     m1, m2 = torch.ones(2, 2, dtype=torch.bool), torch.ones(2, 2, dtype=torch.bool)
     with multirow_attn.tree_mask(m1, torch.tensor([1, 3], dtype=torch.int32)):
-        assert multirow_attn._TREE[0] is m1
+        assert multirow_attn.current_tree()[0] is m1
         with multirow_attn.tree_mask(m2, torch.tensor([1, 3], dtype=torch.int32)):
-            assert multirow_attn._TREE[0] is m2
-        assert multirow_attn._TREE[0] is m1
-    assert multirow_attn._TREE is None
+            assert multirow_attn.current_tree()[0] is m2
+        assert multirow_attn.current_tree()[0] is m1
+    assert multirow_attn.current_tree() is None
 
 
 # ---------------------------------------------------------------- skinny_qmm / small_m_qmm
