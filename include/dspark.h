@@ -97,6 +97,25 @@ int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int bits, int g
  * (template, grid, threadgroup) the Python layer caches per module. Returns a dspark_status. */
 int dspark_qmm_affine_plan(int64_t M, int64_t K, int64_t N, int bits, int group_size, int32_t out[4]);
 
+/*
+ * dspark_qmm_affine without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. Same arguments (minus the workspace), kernels and results,
+ * bit for bit, as dspark_qmm_affine. The split-K counters and partials live in a device array
+ * inside the library, one per GPU, held until the process ends: 256 KiB of counters plus
+ * 32 MiB of partials. A shape whose dspark_qmm_affine_workspace exceeds that is refused with
+ * DSPARK_ERR_WORKSPACE: at M <= 16 that is ceil(N / 64) * S > 8192, with S the K slices
+ * dspark_qmm_affine_plan reports (every projection of a hidden-5120, intermediate-25600 layer
+ * fits; a 151936-row vocabulary head at K = 5120 does not). Nothing is
+ * allocated: the first call on a device looks up the array's address and clears its
+ * counters on `stream`. Every call on one GPU shares the array, so calls that overlap in time
+ * on one GPU (other streams, other host threads) race; order them on one stream.
+ */
+int dspark_qmm_affine_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
+                              const uint32_t* w, const void* scales, const void* biases,
+                              int64_t N, int bits, int group_size,
+                              void* y, int64_t ldy, dspark_stream stream);
+
 /* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size, M and K
  * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,
  * biases and y. Replaces the per-projection QuantizedLinear calls of one decoder layer

@@ -26,6 +26,8 @@
 //     are staged once in LDS and shared by the 4 waves (dspark_qmm_splitk.h). Slices of a
 //     strip are summed by the last workgroup to arrive, in slice order: deterministic and
 //     independent of M. The slice count depends only on the strips and K.
+#include <mutex>
+
 #include "dspark_qmm_splitk.h"
 
 namespace dspark {
@@ -517,4 +519,65 @@ extern "C" int dspark_qmm_workspace_reset(void* workspace, size_t workspace_byte
   const size_t n = workspace_bytes < kCtrRegionBytes ? workspace_bytes : kCtrRegionBytes;
   if (n < sizeof(int)) return DSPARK_OK;
   return zero_counters(workspace, n, static_cast<hipStream_t>(stream), "dspark_qmm_workspace_reset");
+}
+
+// ---- dspark_qmm_affine without a caller workspace: the split-K counters and partials live in
+// a file-scope device array (one copy per GPU, held until the process ends). Host code never
+// passes the array's name to a kernel: it stands in for the symbol on the host. The device
+// address comes from hipGetSymbolAddress, once per device with that device current, and is
+// kept per device.
+namespace dspark {
+namespace {
+constexpr size_t kNoallocPartBytes = 32u << 20;  // fp32 split-K partials
+constexpr size_t kNoallocBytes = kCtrRegionBytes + kNoallocPartBytes;
+static __device__ __align__(256) unsigned char scratch[kNoallocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address of the current device; its counter region is cleared (on `s`, before
+// any use) the first time. Returns a dspark_status.
+int scratch_for_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(DSPARK_ERR_LAUNCH, "qmm_affine_noalloc: no current HIP device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(DSPARK_ERR_LAUNCH, "qmm_affine_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e));
+    const int st = zero_counters(ptr, kCtrRegionBytes, s, "dspark_qmm_affine_noalloc(clear)");
+    if (st) return st;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DSPARK_OK;
+}
+}  // namespace
+}  // namespace dspark
+
+extern "C" int dspark_qmm_affine_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K, const uint32_t* w,
+                                         const void* scales, const void* biases, int64_t N, int bits,
+                                         int group_size, void* y, int64_t ldy, dspark_stream stream) {
+  dspark_qmm_problem p{x, ldx, w, scales, biases, y, ldy, N, K};
+  long Ns[1];
+  int st = validate(&p, 1, M, bits, group_size, Ns);
+  if (st) return st;
+  const Plan pl = make_plan(Ns, 1, K, M, bits);
+  if (pl.S == 0)
+    return fail(DSPARK_ERR_SHAPE, "qmm_affine_noalloc: M=%lld x N=%lld x K=%lld is not supported", (long long)M,
+                (long long)N, (long long)K);
+  const size_t need = pl.ctr_bytes + pl.part_bytes;
+  if (need > kNoallocBytes)
+    return fail(DSPARK_ERR_WORKSPACE,
+                "qmm_affine_noalloc: M=%lld x N=%lld x K=%lld needs %zu bytes of split-K scratch, more than the "
+                "%zu the library holds per GPU; call dspark_qmm_affine with a workspace",
+                (long long)M, (long long)N, (long long)K, need, kNoallocBytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ptr = nullptr;
+  if (need && (st = scratch_for_current_device(s, &ptr))) return st;
+  return multi_impl(&p, 1, M, bits, group_size, false, ptr, need ? kNoallocBytes : 0, s);
 }

@@ -57,3 +57,19 @@ def test_plan_blocks_scale_with_length():
     # every block covers whole 64-key tiles and the blocks cover the cache
     assert lib.dspark_verify_attention_workspace(1, 32, 8, 16, 128, 64) == 0   # one block: no partials
 
+
+def test_noalloc_qmm_refuses_oversize_before_any_gpu_call():
+    """A shape whose split-K scratch exceeds the library-held array is refused on the host
+    (DSPARK_ERR_WORKSPACE) before any HIP call: the pointers below are never dereferenced."""
+    from dspark_rocm import _lib
+
+    lib = _lib.load()
+    N, K, M = 151936, 5120, 16
+    assert lib.dspark_qmm_affine_workspace(M, K, N, 8, 64) > (256 << 10) + (32 << 20)
+    fake = 1 << 20  # 256-byte aligned, non-null; never touched
+    st = lib.dspark_qmm_affine_noalloc(fake, K, M, K, fake, fake, fake, N, 8, 64, fake, N, None)
+    assert st == -4
+    assert b"scratch" in lib.dspark_last_error()
+    # a shape that fits passes the same host checks (it would then need a GPU to launch)
+    assert lib.dspark_qmm_affine_workspace(16, 25600, 5120, 8, 64) <= (256 << 10) + (32 << 20)
+    assert lib.dspark_qmm_affine_workspace(16, 5120, 2 * 25600, 8, 64) <= (256 << 10) + (32 << 20)
