@@ -56,16 +56,38 @@ def qmm(x, lin) -> np.ndarray:
     return bf(qmm_f64(np.asarray(x, dtype=np.float32), w, s, b, bits))
 
 
+def qmm_c(x, lin) -> np.ndarray:
+    """:func:`qmm` through the C restatement (dspark_oracle.c ``orc_qmm``, fp32 factored form,
+    pinned to :func:`qmm_f64` by tests/test_oracle_qmm.py): for matrices too large for the
+    float64 numpy path (a 151936-row vocabulary head, 25600-wide MLPs)."""
+    from . import c_oracle
+    from .quant_ref import bf16_bits
+
+    w, s, b, bits = lin
+    y = c_oracle.qmm(bf16_bits(np.asarray(x, np.float32)), w, bf16_bits(np.asarray(s, np.float32)),
+                     bf16_bits(np.asarray(b, np.float32)), bits)
+    return bf(y)
+
+
 class DenseRef:
     """Weights as numpy: per layer dict of linears (packed uint32, scales, biases (fp32
-    bf16-valued), bits) and norm weights; embed [V, H] fp32 (bf16-valued)."""
+    bf16-valued), bits) and norm weights; embed [V, H] fp32 (bf16-valued), or any object whose
+    ``[ids]`` returns those rows. ``matmul`` evaluates one projection (default :func:`qmm`)."""
 
-    def __init__(self, cfg: dict, embed, layers: list[dict], norm, lm_head):
+    def __init__(self, cfg: dict, embed, layers: list[dict], norm, lm_head, matmul=None):
         self.cfg, self.embed, self.layers, self.norm, self.lm_head = cfg, embed, layers, norm, lm_head
+        self.matmul = matmul or qmm
         c = cfg
         self.k = [np.zeros((c["kv_heads"], 0, c["head_dim"]), np.float32) for _ in layers]
         self.v = [np.zeros((c["kv_heads"], 0, c["head_dim"]), np.float32) for _ in layers]
         self.offset = 0
+
+    def seed_cache(self, keys: list, values: list) -> None:
+        """Start from caches already holding ``keys[l]`` / ``values[l]`` [Hk, L, D] per layer
+        (bf16-valued), e.g. a synthetic prefix; the offset becomes L."""
+        self.k = [np.asarray(k, np.float32) for k in keys]
+        self.v = [np.asarray(v, np.float32) for v in values]
+        self.offset = self.k[0].shape[1]
 
     def forward(self, ids) -> np.ndarray:
         """ids [M] at positions offset..offset+M-1 -> logits [M, V]; appends to the caches."""
@@ -73,7 +95,8 @@ class DenseRef:
         M = len(ids)
         Hq, Hk, D, eps = c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
         pos = np.arange(self.offset, self.offset + M)
-        h = self.embed[np.asarray(ids)]
+        h = np.asarray(self.embed[np.asarray(ids)], np.float32)
+        qmm = self.matmul
         r = None
         for li, L in enumerate(self.layers):
             if r is not None:

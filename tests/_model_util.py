@@ -23,8 +23,9 @@ def _lin(l):
     return (l.weight.detach().cpu().numpy().view(np.uint32), _bf(l.scales), _bf(l.biases), l.bits)
 
 
-def to_ref(model):
-    """The numpy oracle (oracle.model_ref.DenseRef) holding the same weights."""
+def to_ref(model, matmul=None, embed=None):
+    """The numpy oracle (oracle.model_ref.DenseRef) holding the same weights (``embed``: an
+    object whose ``[ids]`` gives the embedding rows, instead of a copy of the whole table)."""
     from oracle.model_ref import DenseRef
 
     a = model.args
@@ -37,4 +38,5 @@ def to_ref(model):
                            gate=_lin(mlp.gate_proj), up=_lin(mlp.up_proj), down=_lin(mlp.down_proj)))
     cfg = dict(heads=a.num_attention_heads, kv_heads=a.num_key_value_heads, head_dim=a.head_dim,
                eps=a.rms_norm_eps, rope_theta=a.rope_theta)
-    return DenseRef(cfg, _bf(model.embed_tokens), layers, _bf(model.norm), _lin(model.lm_head))
+    table = _bf(model.embed_tokens) if embed is None else embed
+    return DenseRef(cfg, table, layers, _bf(model.norm), _lin(model.lm_head), matmul=matmul)

@@ -64,3 +64,21 @@ def test_rollback_equals_fresh_prefix():
     b.forward([1, 2, 3])
     lb = b.forward([9, 10])
     assert np.array_equal(la, lb)
+
+
+def test_c_matmul_and_seeded_cache_agree_with_the_numpy_forward():
+    """qmm_c (the C restatement) lands within one bf16 rounding of the float64 qmm on every
+    projection, and a forward whose caches are seeded with a prefix equals the forward that
+    wrote that prefix itself (the seeded rows are what the earlier forward cached)."""
+    model = tiny_model("cpu", seed=11)
+    r = np.random.Generator(np.random.PCG64(2))
+    lin = to_ref(model).layers[0]["gate"]
+    x = quant_ref.bf16_round(r.standard_normal((5, model.args.hidden_size)).astype(np.float32))
+    a, b = model_ref.qmm(x, lin), model_ref.qmm_c(x, lin)
+    assert np.all(np.abs(a - b) <= 2 ** -7 * np.abs(a) + 1e-6)
+    full = to_ref(model, matmul=model_ref.qmm_c)
+    full.forward([4, 8, 15, 16, 23])
+    seeded = to_ref(model, matmul=model_ref.qmm_c)
+    seeded.seed_cache([k[:, :5] for k in full.k], [v[:, :5] for v in full.v])
+    assert seeded.offset == 5
+    assert np.array_equal(seeded.forward([42, 7]), full.forward([42, 7]))
