@@ -31,6 +31,12 @@ extern "C" {
 
 typedef void* dspark_stream; /* hipStream_t */
 
+/* Element type of an activation / KV tensor (verify attention). */
+enum dspark_dtype {
+  DSPARK_DTYPE_BF16 = 0,
+  DSPARK_DTYPE_F16 = 1
+};
+
 enum dspark_status {
   DSPARK_OK = 0,
   DSPARK_ERR_ARG = -1,       /* null pointer or bad enum value */
@@ -216,7 +222,7 @@ size_t dspark_qmm_swiglu_packed_workspace(int64_t N, int64_t K, int64_t M, int b
  * out      bf16 [B, Hq, Mq, D] contiguous
  * workspace  device buffer of at least dspark_verify_attention_workspace(...) bytes
  *            (fp32 split-KV partials); may be NULL when that size is 0.
- * D in {64, 128}; Hq % Hk == 0; gqa * Mq <= 256.
+ * D in {64, 128, 256}; Hq % Hk == 0; gqa * Mq <= 256.
  *
  * Replaces multirow_attn.multirow_sdpa(q, k, v, scale=, causal=, tree_anc=)
  * (multirow_attn.py:223-259): the dspark_mra_p1 / _p1_tree / _p2 Metal kernels
@@ -244,6 +250,41 @@ int dspark_verify_attention_strided(const void* q, int64_t B, int64_t Hq, int64_
                                     int causal, const uint32_t* tree_anc, void* out,
                                     const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
                                     dspark_stream stream);
+
+/* dspark_verify_attention_strided for bf16 (dtype DSPARK_DTYPE_BF16) or fp16
+ * (DSPARK_DTYPE_F16) q, K, V and output: the reference serves both (multirow_attn.py:294-307,
+ * its kernel templated on the input type, :180-197). P is rounded to the input type for P.V;
+ * accumulation is fp32 either way. */
+int dspark_verify_attention_typed(int dtype, const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
+                                  const void* k, const void* v, const int64_t k_strides[3],
+                                  const int64_t v_strides[3], int64_t Hk, int64_t L_total, float scale,
+                                  int causal, const uint32_t* tree_anc, void* out,
+                                  const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
+                                  dspark_stream stream);
+
+/*
+ * Verify attention over a quantized KV cache: the state of mlx-lm's QuantizedKVCache, which
+ * the reference's targets build when kv_bits is set (target.py:166-184; its shape is read back
+ * at calibrate.py:225-238). K and V are each
+ *   words   uint32 [B, Hk, L, D*bits/32]: fields of `bits` (4 or 8) along D, low bits first
+ *           (the affine layout of dspark_qmm_affine); strides k_strides / v_strides in words
+ *           (each a multiple of 4; the last dim contiguous);
+ *   scales, biases  [B, Hk, L, D/group_size] of the q dtype, one pair per 64 values of a row
+ *           (strides k_scale_strides / v_scale_strides in elements, shared by scales and biases).
+ * Each value is scale * field + bias (group_size 64). The reference's own multirow kernel does
+ * not read this format (quantized caches fall through to mlx-lm's quantized SDPA,
+ * multirow_attn.py:288-299); this entry point serves that fall-through on the same kernel: the
+ * tile loader dequantizes to the compute type (fp32 fma, one rounding) and the MFMA loop, mask,
+ * softmax and split-KV combine are those of dspark_verify_attention_typed. No tree mask.
+ */
+int dspark_verify_attention_quantized(int dtype, const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
+                                      const uint32_t* k_words, const void* k_scales, const void* k_biases,
+                                      const int64_t k_strides[3], const int64_t k_scale_strides[3],
+                                      const uint32_t* v_words, const void* v_scales, const void* v_biases,
+                                      const int64_t v_strides[3], const int64_t v_scale_strides[3], int64_t Hk,
+                                      int64_t L_total, float scale, int causal, int bits, int group_size, void* out,
+                                      const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
+                                      dspark_stream stream);
 
 /* Launch geometry of dspark_verify_attention (host-only query): out[0] rows R = gqa * Mq,
  * out[1] padded rows RP, out[2] row groups NRG, out[3] keys per block CHUNK, out[4] key

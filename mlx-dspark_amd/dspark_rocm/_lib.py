@@ -112,6 +112,14 @@ SIGNATURES: dict[str, tuple] = {
     "dspark_verify_attention_strided": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_i64_p,
                                                 c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p, c_i64_p,
                                                 c_void_p, c_size_t, c_void_p]),
+    "dspark_verify_attention_typed": (c_int, [c_int, c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p,
+                                              c_i64_p, c_i64_p, c_i64, c_i64, c_float, c_int, c_void_p, c_void_p,
+                                              c_i64_p, c_void_p, c_size_t, c_void_p]),
+    "dspark_verify_attention_quantized": (c_int, [c_int, c_void_p, c_i64, c_i64, c_i64, c_i64,
+                                                  c_void_p, c_void_p, c_void_p, c_i64_p, c_i64_p,
+                                                  c_void_p, c_void_p, c_void_p, c_i64_p, c_i64_p,
+                                                  c_i64, c_i64, c_float, c_int, c_int, c_int, c_void_p, c_i64_p,
+                                                  c_void_p, c_size_t, c_void_p]),
     "dspark_verify_attention_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "dspark_verify_attention_blocks": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "dspark_verify_attention_plan": (c_int, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,

@@ -66,3 +66,24 @@ def scaled_dot_product_attention(q, k, v, *, scale, mask=None, sinks=None, **kw)
 
 
 STOCK = scaled_dot_product_attention
+
+
+def quantized_scaled_dot_product_attention(q, q_keys, q_values, *, scale, mask=None, group_size: int = 64,
+                                           bits: int = 8):
+    """Attention over quantized K/V triples (words, scales, biases), the helper mlx-lm's
+    attention layers call when their cache has ``bits``: the stock path dequantizes
+    (``scale * field + bias`` in fp32) and runs :func:`scaled_dot_product_attention` in fp32,
+    output in q's dtype. Patchable like the plain entry point."""
+    from .quant import unpack
+
+    def deq(trip):
+        w, s, b = trip
+        lead = w.shape[:-1]
+        vals = unpack(w.reshape(-1, w.shape[-1]), bits).to(torch.float32).reshape(*lead, -1)
+        g = vals.reshape(*lead, -1, group_size)
+        return (g * s.to(torch.float32).unsqueeze(-1) + b.to(torch.float32).unsqueeze(-1)).reshape(*lead, -1)
+
+    return _stock_sdpa(q.to(torch.float32), deq(q_keys), deq(q_values), scale=scale, mask=mask).to(q.dtype)
+
+
+QUANTIZED_STOCK = quantized_scaled_dot_product_attention

@@ -1,19 +1,23 @@
 """Multi-row verify attention: the gfx950 kernel behind the reference's ``multirow_sdpa`` and
-its scoped patch of the attention entry point.
+its scoped patch of the attention entry points (plain and quantized-cache).
 
 Same API as the reference module (multirow_attn.py:204-488): ``plan``, ``multirow_sdpa``,
 ``Window``, ``MultirowConfig``, ``eligible``, ``tree_mask``, ``multirow_attention``,
-``active`` and ``measure_window``. The kernel is ``dspark_verify_attention`` (split-KV pass
-plus combine, v_mfma_f32_16x16x32_bf16); it serves bf16, head_dim 64 or 128, whole GQA groups
-with gqa * q_len <= 256, and reads K/V through their batch/head/sequence strides (KV-cache
-views sliced along the sequence axis are used in place).
+``active`` and ``measure_window``. The kernel is ``dspark_verify_attention_typed`` (split-KV
+pass plus combine, v_mfma_f32_16x16x32_{bf16,f16}); it serves bf16 and fp16, head_dim 64, 128
+or 256 (the reference's D <= 256, multirow_attn.py:200-214, :294-307), whole GQA groups with
+gqa * q_len <= 256, and reads K/V through their batch/head/sequence strides (KV-cache views
+sliced along the sequence axis are used in place). ``quantized_sdpa`` runs the same kernel
+over mlx-lm's quantized-cache triples (``dspark_verify_attention_quantized``).
 
 ``multirow_attention(cfg)`` patches :func:`dspark_rocm.fast.scaled_dot_product_attention`:
 an eligible call of a measured shape (its :class:`Window`) runs the kernel — causal iff the
 mask is the string "causal" and q_len > 1 — and every other call falls through to whatever
 was installed before (the split scope, then the stock path) (multirow_attn.py:338-370). A
 tree verify registers its exact mask object with :func:`tree_mask`; calls carrying that
-object take the kernel's ancestry variant (multirow_attn.py:322-349).
+object take the kernel's ancestry variant (multirow_attn.py:322-349). The scope also patches
+:func:`dspark_rocm.fast.quantized_scaled_dot_product_attention`, mlx-lm's helper for caches
+with ``bits``, so a quantized cache of a measured shape runs the kernel too.
 """
 
 from __future__ import annotations
@@ -29,10 +33,10 @@ from . import _lib, _scope, fast, gate, ops
 
 _STOCK = fast.STOCK
 
-MAX_D = 128
+MAX_D = 256
 HEAD_DIMS = ops.ATTN_HEAD_DIMS
 MAX_ROWS = 256          # gqa * q_len the kernel's row tiles cover
-_DTYPES = (torch.bfloat16,)
+_DTYPES = tuple(ops.ATTN_DTYPES)
 
 
 def plan(hq: int, hk: int, q_len: int, d: int, kv_len: int, batch: int = 1) -> dict:
@@ -42,6 +46,14 @@ def plan(hq: int, hk: int, q_len: int, d: int, kv_len: int, batch: int = 1) -> d
     _lib.check("dspark_verify_attention_plan",
                _lib.load().dspark_verify_attention_plan(batch, hq, hk, q_len, d, kv_len, out))
     return {"R": out[0], "RP": out[1], "NRG": out[2], "CHUNK": out[3], "NB": out[4], "workgroups": out[5]}
+
+
+def quantized_sdpa(q: torch.Tensor, q_keys, q_values, *, scale: float, causal: bool, group_size: int = 64,
+                   bits: int = 8) -> torch.Tensor:
+    """The kernel over quantized K/V triples (words, scales, biases) of mlx-lm's
+    ``QuantizedKVCache`` (``ops.verify_attention_quantized``)."""
+    return ops.verify_attention_quantized(q, q_keys, q_values, scale=scale, causal=causal, bits=bits,
+                                          group_size=group_size)
 
 
 def multirow_sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, causal: bool,
@@ -123,6 +135,7 @@ def eligible(q, k, v, mask, sinks, cfg: MultirowConfig) -> bool:
 # Scope state: the active config, what the patch falls through to, the registered tree mask.
 _config = _scope.Slot()
 _fallthrough = _scope.Slot()
+_fallthrough_q = _scope.Slot()
 _tree = _scope.Slot()
 
 
@@ -152,6 +165,37 @@ def _route(q, k, v, scale, mask, sinks, cfg):
     return None
 
 
+def why_not_quantized(q, q_keys, q_values, mask, cfg: MultirowConfig, group_size: int, bits: int) -> str | None:
+    """:func:`why_not` for a quantized-cache call: the same window and shape rules, on the
+    (words, scales, biases) triples."""
+    if bits not in ops.KV_BITS or group_size != 64:
+        return "format"
+    kw, ks, kb = q_keys
+    vw, vs, vb = q_values
+    if not (kw.dim() == vw.dim() == ks.dim() == 4):
+        return "rank"
+    D = q.shape[-1] if q.dim() == 4 else 0
+    k_like = torch.empty((kw.shape[0], kw.shape[1], kw.shape[2], D), dtype=ks.dtype, device="meta")
+    reason = why_not(q, k_like, k_like, mask, None, cfg)
+    if reason:
+        return reason
+    if kw.shape[-1] * 32 // bits != D or tuple(vw.shape) != tuple(kw.shape):
+        return "head_dim"
+    if not (ks.dtype == kb.dtype == vs.dtype == vb.dtype == q.dtype):
+        return "dtype"
+    return None
+
+
+def _patched_quantized(q, q_keys, q_values, *, scale, mask=None, group_size: int = 64, bits: int = 8):
+    cfg = _config.value
+    if (cfg is not None and q.is_cuda and q_keys[0].is_cuda
+            and why_not_quantized(q, q_keys, q_values, mask, cfg, group_size, bits) is None):
+        return quantized_sdpa(q, q_keys, q_values, scale=scale, causal=mask == "causal" and q.shape[2] > 1,
+                              group_size=group_size, bits=bits)
+    below = _fallthrough_q.value or fast.QUANTIZED_STOCK
+    return below(q, q_keys, q_values, scale=scale, mask=mask, group_size=group_size, bits=bits)
+
+
 def _patched_call(q, k, v, *, scale, mask=None, sinks=None, **kw):
     cfg = _config.value
     out = _route(q, k, v, scale, mask, sinks, cfg) if cfg is not None and not kw else None
@@ -169,9 +213,10 @@ def multirow_attention(cfg: MultirowConfig | None):
     if cfg is None or active():
         yield
         return
-    below = fast.scaled_dot_product_attention
-    with _config.holding(cfg), _fallthrough.holding(below), \
-            _scope.replaced(fast, "scaled_dot_product_attention", _patched_call):
+    below, below_q = fast.scaled_dot_product_attention, fast.quantized_scaled_dot_product_attention
+    with _config.holding(cfg), _fallthrough.holding(below), _fallthrough_q.holding(below_q), \
+            _scope.replaced(fast, "scaled_dot_product_attention", _patched_call), \
+            _scope.replaced(fast, "quantized_scaled_dot_product_attention", _patched_quantized):
         yield
 
 

@@ -354,7 +354,9 @@ def _pick(ws: torch.Tensor | None, device, nbytes: int, qmm: bool):
 
 # ---------------------------------------------------------------------------- verify attention
 
-ATTN_HEAD_DIMS = (64, 128)
+ATTN_HEAD_DIMS = (64, 128, 256)
+ATTN_DTYPES = {torch.bfloat16: 0, torch.float16: 1}   # dspark_dtype codes
+KV_BITS = (4, 8)
 
 
 def _i64x3(t: torch.Tensor):
@@ -362,17 +364,17 @@ def _i64x3(t: torch.Tensor):
     return arr
 
 
-def verify_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, causal: bool = True,
-                     tree_anc: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``softmax(scale * q k^T + mask) v`` for few verify rows over a (strided) KV cache view.
+def _attn_dtype(q: torch.Tensor, *others: torch.Tensor) -> int:
+    if q.dtype not in ATTN_DTYPES:
+        raise TypeError(f"verify attention: q dtype {q.dtype} (bfloat16 or float16)")
+    for t in others:
+        if t.dtype != q.dtype:
+            raise TypeError(f"verify attention: {t.dtype} does not match q's {q.dtype}")
+    return ATTN_DTYPES[q.dtype]
 
-    q bf16 [B, Hq, Mq, D]; k/v bf16 [B, Hk, L, D] with unit stride along D (any batch/head/seq
-    strides, e.g. a ``[..., :L, :]`` slice of a larger cache). ``causal``: row i sees keys
-    ``0 .. L - Mq + i``. ``tree_anc`` (uint32/int32 [Mq]) selects the tree-verify mask.
-    """
-    _require_cuda(q, k, v)
+
+def _attn_shapes(q, k, v):
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _require_bf16(name, t)
         if t.dim() != 4:
             raise ValueError(f"{name}: expected [B, H, L, D]")
     B, Hq, mq, D = q.shape
@@ -381,23 +383,82 @@ def verify_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale
         raise ValueError(f"k/v must be [{B}, Hk, L, {D}]; got {tuple(k.shape)} / {tuple(v.shape)}")
     if k.stride(-1) != 1 or v.stride(-1) != 1:
         raise ValueError("k/v must be contiguous along head_dim")
+    return B, Hq, mq, D, Hk, L
+
+
+def verify_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, causal: bool = True,
+                     tree_anc: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``softmax(scale * q k^T + mask) v`` for few verify rows over a (strided) KV cache view.
+
+    q bf16 or fp16 [B, Hq, Mq, D] (D in 64, 128, 256); k/v of q's dtype [B, Hk, L, D] with unit
+    stride along D (any batch/head/seq strides, e.g. a ``[..., :L, :]`` slice of a larger
+    cache). ``causal``: row i sees keys ``0 .. L - Mq + i``. ``tree_anc`` (uint32/int32 [Mq])
+    selects the tree-verify mask.
+    """
+    _require_cuda(q, k, v)
+    dt = _attn_dtype(q, k, v)
+    B, Hq, mq, D, Hk, L = _attn_shapes(q, k, v)
     q = q.contiguous()
-    lib = _lib.load()
     if out is None:
         out = torch.empty_like(q)
-    nbytes = lib.dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
-    ws = workspace(q.device, nbytes)
-    anc = None
-    if tree_anc is not None:
-        anc = tree_anc.to(device=q.device, dtype=torch.int32).contiguous()
-    _lib.call("dspark_verify_attention", _ptr(q), B, Hq, mq, D, _ptr(k), _ptr(v), _i64x3(k), _i64x3(v), Hk, L,
-              float(scale), int(bool(causal)), _ptr(anc), _ptr(out), _ptr(ws), 0 if ws is None else ws.numel(),
-              _stream(q))
+    osr = (ctypes.c_int64 * 3)(Hq * mq * D, mq * D, D)
+    return _launch_attention(dt, q, k, v, out, osr, scale, causal, tree_anc, None)
+
+
+def _launch_attention(dt, q, k, v, out, out_strides, scale, causal, tree_anc, ws):
+    B, Hq, mq, D = q.shape
+    Hk, L = k.shape[1], k.shape[2]
+    nbytes = _lib.load().dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
+    ws = _pick(ws, q.device, nbytes, qmm=False)
+    anc = None if tree_anc is None else tree_anc.to(device=q.device, dtype=torch.int32).contiguous()
+    _lib.call("dspark_verify_attention_typed", dt, _ptr(q), B, Hq, mq, D, _ptr(k), _ptr(v), _i64x3(k), _i64x3(v),
+              Hk, L, float(scale), int(bool(causal)), _ptr(anc), _ptr(out), out_strides, _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(q))
     return out
 
 
 def verify_attention_blocks(B: int, Hq: int, Hk: int, mq: int, D: int, L: int) -> int:
     return int(_lib.load().dspark_verify_attention_blocks(B, Hq, Hk, mq, D, L))
+
+
+def verify_attention_quantized(q: torch.Tensor, keys, values, *, scale: float, causal: bool = True, bits: int = 8,
+                               group_size: int = GROUP, out: torch.Tensor | None = None,
+                               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Verify attention over a quantized KV cache (mlx-lm ``QuantizedKVCache`` state).
+
+    ``keys`` / ``values`` = (words int32 [B, Hk, L, D*bits/32], scales [B, Hk, L, D/64],
+    biases [B, Hk, L, D/64]) with scales/biases in q's dtype, fields of ``bits`` (4 or 8)
+    along D, low bits first; any batch/head/seq strides (cache views), unit stride along the
+    last dim. Semantics: attention over ``scale * q_field + bias`` per group of 64 values.
+    """
+    kw, ks, kb = keys
+    vw, vs, vb = values
+    _require_cuda(q, kw, ks, kb, vw, vs, vb)
+    dt = _attn_dtype(q, ks, kb, vs, vb)
+    if bits not in KV_BITS:
+        raise ValueError(f"bits={bits} (4 or 8)")
+    for t in (kw, vw):
+        _require_packed(t)
+    B, Hq, mq, D = q.shape
+    Hk, L = kw.shape[1], kw.shape[2]
+    W, G = D * bits // 32, D // group_size
+    for name, t, last in (("key words", kw, W), ("value words", vw, W), ("key scales", ks, G), ("key biases", kb, G),
+                          ("value scales", vs, G), ("value biases", vb, G)):
+        if t.dim() != 4 or tuple(t.shape) != (B, Hk, L, last) or t.stride(-1) != 1:
+            raise ValueError(f"{name}: expected [{B}, {Hk}, {L}, {last}] with unit last stride, got {tuple(t.shape)}")
+    if ks.stride() != kb.stride() or vs.stride() != vb.stride():
+        raise ValueError("scales and biases of one cache must share strides")
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    osr = (ctypes.c_int64 * 3)(Hq * mq * D, mq * D, D)
+    nbytes = _lib.load().dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
+    ws = _pick(workspace, q.device, nbytes, qmm=False)
+    _lib.call("dspark_verify_attention_quantized", dt, _ptr(q), B, Hq, mq, D, _ptr(kw), _ptr(ks), _ptr(kb), _i64x3(kw),
+              _i64x3(ks), _ptr(vw), _ptr(vs), _ptr(vb), _i64x3(vw), _i64x3(vs), Hk, L, float(scale),
+              int(bool(causal)), bits, group_size, _ptr(out), osr, _ptr(ws), 0 if ws is None else ws.numel(),
+              _stream(q))
+    return out
 
 
 # ---------------------------------------------------------------------------- MoE
@@ -481,17 +542,11 @@ def verify_attention_into(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out
     """:func:`verify_attention` writing through element strides ``out_strides`` = (batch, query
     head, position) of ``out`` (head_dim contiguous), e.g. [B, Mq, Hq*D] rows for o_proj."""
     _require_cuda(q, k, v, out)
-    B, Hq, mq, D = q.shape
-    Hk, L = k.shape[1], k.shape[2]
+    dt = _attn_dtype(q, k, v, out)
+    _attn_shapes(q, k, v)
     q = q.contiguous()
-    nbytes = _lib.load().dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
-    ws = _pick(workspace, q.device, nbytes, qmm=False)
-    anc = None if tree_anc is None else tree_anc.to(device=q.device, dtype=torch.int32).contiguous()
-    os_ = (ctypes.c_int64 * 3)(*[int(s) for s in out_strides])
-    _lib.call("dspark_verify_attention_strided", _ptr(q), B, Hq, mq, D, _ptr(k), _ptr(v), _i64x3(k), _i64x3(v), Hk, L,
-              float(scale), int(bool(causal)), _ptr(anc), _ptr(out), os_, _ptr(ws), 0 if ws is None else ws.numel(),
-              _stream(q))
-    return out
+    osr = (ctypes.c_int64 * 3)(*[int(x) for x in out_strides])
+    return _launch_attention(dt, q, k, v, out, osr, scale, causal, tree_anc, workspace)
 
 
 # ---------------------------------------------------------------------------- verify-forward layer ops

@@ -75,6 +75,26 @@ def quantize(w: torch.Tensor, group_size: int = GROUP, bits: int = 4):
     return pack(q, bits), scale.contiguous(), bias.contiguous()
 
 
+def quantize_rows(x: torch.Tensor, bits: int, group_size: int = GROUP, dtype=torch.bfloat16):
+    """Quantize the last dim of ``x`` [..., D] with the rule of :func:`quantize` (scales and
+    biases rounded to ``dtype``): (words int32 [..., D*bits/32], scales [..., D/gs], biases)."""
+    lead, d = x.shape[:-1], x.shape[-1]
+    _check(bits, group_size)
+    if d % group_size:
+        raise ValueError(f"D={d} is not a multiple of {group_size}")
+    xg = x.reshape(-1, d // group_size, group_size).to(torch.float32)
+    lo, hi = xg.amin(dim=-1), xg.amax(dim=-1)
+    levels = (1 << bits) - 1
+    scale = ((hi - lo) / levels).to(dtype)
+    bias = lo.to(dtype)
+    s32 = scale.to(torch.float32)
+    s_safe = torch.where(s32 == 0, torch.ones_like(s32), s32)
+    q = torch.round((xg - bias.to(torch.float32).unsqueeze(-1)) / s_safe.unsqueeze(-1)).clamp_(0, levels)
+    words = pack(q.to(torch.int32).reshape(-1, d), bits)
+    return (words.reshape(*lead, d * bits // 32), scale.reshape(*lead, d // group_size),
+            bias.reshape(*lead, d // group_size))
+
+
 def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = GROUP,
                bits: int = 4) -> torch.Tensor:
     """Packed weights -> fp32 [N, K] (``scale*q + bias`` in fp32)."""

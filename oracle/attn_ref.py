@@ -137,3 +137,22 @@ def split_sdpa(q, k, v, scale: float, causal: bool, max_chunk: int) -> np.ndarra
             outs.append(attention(qc, k, v, scale, causal=False))
         off += p
     return np.concatenate(outs, axis=2)
+
+
+def dequantize_kv(words, scales, biases, bits: int) -> np.ndarray:
+    """Quantized cache rows (mlx-lm QuantizedKVCache: uint32 words [..., L, D*bits/32] of
+    ``bits``-wide fields along D, low bits first; scales/biases [..., L, D/64]) -> float64
+    [..., L, D] = scale * field + bias per group of 64 (the affine format of quant_ref)."""
+    from .quant_ref import dequantize
+
+    w = np.asarray(words).view(np.uint32)
+    lead = w.shape[:-1]
+    flat = dequantize(w.reshape(-1, w.shape[-1]), np.asarray(scales, np.float64).reshape(-1, scales.shape[-1]),
+                      np.asarray(biases, np.float64).reshape(-1, biases.shape[-1]), bits)
+    return flat.reshape(*lead, -1)
+
+
+def attention_quantized(q, keys, values, scale: float, bits: int, causal: bool = True) -> np.ndarray:
+    """float64 attention over dequantized K/V triples (words, scales, biases): the function the
+    quantized-KV attention computes (dequantize, then the definition of :func:`attention`)."""
+    return attention(q, dequantize_kv(*keys, bits), dequantize_kv(*values, bits), scale, causal=causal)

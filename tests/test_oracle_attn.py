@@ -126,3 +126,29 @@ def test_c_restatement_matches(tree):
     got = c_oracle.attention(quant_ref.bf16_bits(q), quant_ref.bf16_bits(k), quant_ref.bf16_bits(v), 0.125,
                              causal=not tree, tree_anc=anc)
     assert np.abs(got - exact).max() <= 2e-2 * np.sqrt(np.mean(exact ** 2))
+
+
+def test_quantized_kv_oracle_pins():
+    """dequantize_kv is the affine format row by row: unit scales and zero biases give the
+    integer fields themselves (an integer-valued cache, attended exactly like plain K/V);
+    general scales/biases match the per-row dequantize of quant_ref; attention_quantized is
+    attention over those values."""
+    from oracle import quant_ref
+
+    r = np.random.Generator(np.random.PCG64(9))
+    for bits in (4, 8):
+        B, H, L, D = 1, 2, 37, 128
+        ints = r.integers(0, 1 << bits, (B * H * L, D))
+        words = quant_ref.pack(ints, bits).reshape(B, H, L, D * bits // 32)
+        ones = np.ones((B, H, L, D // 64), np.float32)
+        zeros = np.zeros_like(ones)
+        assert np.array_equal(attn_ref.dequantize_kv(words, ones, zeros, bits), ints.reshape(B, H, L, D))
+        s = quant_ref.bf16_round(r.uniform(0.01, 0.1, (B, H, L, D // 64)).astype(np.float32))
+        b = quant_ref.bf16_round(r.normal(0, 0.5, (B, H, L, D // 64)).astype(np.float32))
+        got = attn_ref.dequantize_kv(words, s, b, bits)
+        want = ints.reshape(B, H, L, 2, 64) * s[..., None].astype(np.float64) + b[..., None]
+        assert np.allclose(got, want.reshape(B, H, L, D), rtol=0, atol=0)
+        q = r.standard_normal((B, 4, 5, D))
+        vals = (words, s, b)
+        plain = attn_ref.attention(q, got, got, 0.1, causal=True)
+        assert np.array_equal(attn_ref.attention_quantized(q, vals, vals, 0.1, bits, causal=True), plain)
