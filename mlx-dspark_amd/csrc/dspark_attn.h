@@ -118,8 +118,9 @@ inline Plan make_plan(long B, long Hq, long Hk, long Mq, long D, long L) {
   p.R = (int)((Hq / Hk) * Mq);
   p.RT = (p.R + 15) / 16;
   p.RP = p.RT * 16;
-  // head dim 256 runs two waves per row tile: at most 4 row tiles (512 threads) per workgroup
-  p.WV = (p.RT > 4 && D <= 128) ? 8 : 4;
+  // head dim 256 runs two waves per row tile: up to 6 row tiles (12 waves of <= 168 VGPRs,
+  // three per SIMD), so a 24/4-head group's 96 rows share one pass over K/V
+  p.WV = p.RT > 4 ? (D <= 128 ? 8 : 6) : 4;
   p.KS = 1;
   p.PF = p.WV == 8 ? 2 : 1;
   p.NRG = (p.RT + p.WV - 1) / p.WV;
@@ -220,8 +221,9 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   constexpr int DH = D / DS;          // output columns per wave
   constexpr int KP = D + 8;           // padded K row (elements)
   constexpr int DC = D / 8;           // 16-byte chunks of a T row
-  constexpr int LOADS = KT * DC / THREADS;  // 16-byte K chunks per thread per tile (plain)
-  static_assert(LOADS >= 1 && KT * DC % THREADS == 0 && THREADS % DC == 0, "K tile split");
+  constexpr int LOADS = (KT * DC + THREADS - 1) / THREADS;  // 16-byte K chunks per thread per tile (plain)
+  constexpr bool KPART = LOADS * THREADS != KT * DC;       // the last round covers part of the threads
+  static_assert(THREADS % DC == 0, "K tile split");
   constexpr int NDC = D / 32;         // d-chunks of the S MFMA
   constexpr int NDT = DH / 16;        // d-tiles of the O MFMA per wave
   constexpr int VQ = KT / 4;          // 4-key quads of a V tile
@@ -314,7 +316,8 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
       const char* kb = reinterpret_cast<const char*>(kbase16 + (long)kt * a.kss);
       const char* vb = reinterpret_cast<const char*>(vbase16 + (long)kt * a.vss);
 #pragma unroll
-      for (int j = 0; j < LOADS; ++j) r.k[j] = ldg128((kb + j * kstep) + koff);
+      for (int j = 0; j < LOADS; ++j)
+        if (!KPART || tid + THREADS * j < KT * DC) r.k[j] = ldg128((kb + j * kstep) + koff);
       if (vthread) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) r.v[j] = ldg128((vb + (long)j * a.vss * 2) + voff);
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
     }
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      const int c = tid + THREADS * j;
+      const int c = min(tid + THREADS * j, KT * DC - 1);
       const int key = min(kt + c / DC, L - 1);
       r.k[j] = ldg128(kbase16 + (long)key * a.kss + 8 * (c % DC));
     }
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) {
         const int c = tid + THREADS * j;
-        *reinterpret_cast<u32x4_t*>(&ks_lds[(c / DC) * KP + 8 * (c % DC)]) = r.k[j];
+        if (!KPART || c < KT * DC) *reinterpret_cast<u32x4_t*>(&ks_lds[(c / DC) * KP + 8 * (c % DC)]) = r.k[j];
       }
     }
     if (vthread) {
@@ -776,11 +779,18 @@ int launch_impl(const AttnArgs& a, const Plan& p, long B, bool tree, int qbits, 
   else if (p.KS == 2) DSPARK_P1(TR, 4, 2, 1, Q); \
   else DSPARK_P1(TR, 4, 1, 1, Q);
   if constexpr (D == 256) {
-    // two waves per row tile; at most 4 row tiles, no key split
-    if (qbits == 8) DSPARK_P1(false, 4, 1, 1, 8);
-    else if (qbits == 4) DSPARK_P1(false, 4, 1, 1, 4);
-    else if (tree) DSPARK_P1(true, 4, 1, 1, 0);
-    else DSPARK_P1(false, 4, 1, 1, 0);
+    // two waves per row tile, no key split; 4 or 6 row tiles (quantized K/V: always 4, whose
+    // registers do not fit three waves per SIMD; the same key blocks and partial layout, so
+    // the workspace is the plan's, with one more row group when there are more than 4 tiles)
+    const dim3 grid4((unsigned)(B * a.Hk), (unsigned)p.NB, (unsigned)((a.RT + 3) / 4));
+#define DSPARK_P1_4(TR, Q) \
+  hipLaunchKernelGGL((p1_kernel<T, D, TR, 4, 1, 1, Q>), grid4, dim3(64 * 4 * DS), 0, s, a)
+    if (qbits == 8) DSPARK_P1_4(false, 8);
+    else if (qbits == 4) DSPARK_P1_4(false, 4);
+    else if (p.WV == 6) { if (tree) DSPARK_P1(true, 6, 1, 1, 0); else DSPARK_P1(false, 6, 1, 1, 0); }
+    else if (tree) DSPARK_P1_4(true, 0);
+    else DSPARK_P1_4(false, 0);
+#undef DSPARK_P1_4
   } else {
     if (qbits == 8) { DSPARK_P1_W(false, 8) }
     else if (qbits == 4) { DSPARK_P1_W(false, 4) }

@@ -68,6 +68,8 @@ D256 = [
     (2, 8, 8, 5, 129, True),        # MHA, batch 2
     (1, 4, 1, 3, 23, True),         # tail shorter than a tile
     (1, 32, 2, 4, 700, True),       # GQA 16
+    (1, 32, 4, 16, 900, True),      # 128 rows: 6-tile workgroups, two row groups
+    (1, 40, 4, 10, 640, True),      # 100 rows: one 6-tile workgroup, partly filled
 ]
 
 
@@ -150,6 +152,7 @@ QCASES = [
     (1, 32, 8, 16, 600, 128, True),      # short cache: key-split workgroups
     (2, 8, 8, 5, 129, 64, True),         # batch 2, D 64
     (1, 16, 8, 16, 1500, 256, False),    # D 256, non-causal
+    (1, 24, 4, 16, 1100, 256, True),     # D 256, 96 rows: the quantized path's 4-tile row groups
     (1, 4, 1, 3, 23, 64, True),          # tail shorter than a tile
 ]
 
