@@ -213,3 +213,33 @@ def test_switch_glu_and_sparse_moe_block_match_oracle(dev, M):
     unfused = block.forward_unfused(x)
     assert_rms_close(_np(fused), ref, 2e-2, "SparseMoeBlock fused")
     assert_rms_close(_np(unfused), ref, 2e-2, "SparseMoeBlock unfused")
+
+
+def test_apply_wiring_measures_and_routes(dev, tmp_path, monkeypatch):
+    """The load-time wiring end to end on this GPU: apply_small_m and apply_multirow_attn race
+    the real kernels for a model's shapes (hidden 1024, intermediate 4096, 8/2 heads x 128),
+    cache the verdicts, and verify_scopes then routes the module path through the kernels; its
+    logits match the fused engine's."""
+    from _model_util import tiny_model
+
+    from dspark_rocm import calibrate, multirow_attn, small_m_qmm
+    from dspark_rocm.model import Target
+
+    monkeypatch.setenv("DSPARK_CACHE_DIR", str(tmp_path))
+    monkeypatch.setattr(calibrate, "SMALL_M_IDS", None)
+    monkeypatch.setattr(calibrate, "MULTIROW_CFG", None)
+    model = tiny_model(dev, seed=12, hidden_size=1024, intermediate_size=4096, num_attention_heads=8,
+                       num_key_value_heads=2)
+    ids = calibrate.apply_small_m(model, target_repo="synthetic-1024", verbose=True)
+    cfg = calibrate.apply_multirow_attn(model, verbose=True)
+    assert ids, "the small-M kernel should win on a 1024 x 4096 8-bit model on MI355X"
+    assert cfg is not None and cfg.window(8, 2, 128) is not None
+    assert len(list(tmp_path.iterdir())) >= 2                      # both verdicts cached
+    tgt = Target(model)
+    ids_t = torch.tensor([[7, 1, 8, 2, 8, 1, 8, 2, 8, 4, 5, 9, 0, 4, 5, 2]])
+    fused, _ = tgt.verify(ids_t, tgt.make_cache(64))
+    cb = tgt.make_cache(64)
+    with calibrate.verify_scopes(), torch.no_grad():
+        assert small_m_qmm.active() and multirow_attn.active()
+        mod = model(ids_t.to(dev), cb)
+    assert_rms_close(_np(mod[0]), _np(fused[0]), 5e-2, "module path under the applied scopes vs fused")
