@@ -34,7 +34,8 @@ typedef void* dspark_stream; /* hipStream_t */
 /* Element type of an activation / KV tensor (verify attention). */
 enum dspark_dtype {
   DSPARK_DTYPE_BF16 = 0,
-  DSPARK_DTYPE_F16 = 1
+  DSPARK_DTYPE_F16 = 1,
+  DSPARK_DTYPE_F32 = 2   /* dspark_qmm_dequantize only */
 };
 
 enum dspark_status {
@@ -121,6 +122,18 @@ int dspark_qmm_affine_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
                               const uint32_t* w, const void* scales, const void* biases,
                               int64_t N, int bits, int group_size,
                               void* y, int64_t ldy, dspark_stream stream);
+
+/*
+ * Dequantize once, for the prefill wide path: out[n, j] = (scale[n, j/64] * q[n, j]) + bias[n, j/64]
+ * for the reference-layout matrix of dspark_qmm_affine, each operation an fp32 operation rounded
+ * to nearest (no fma), then stored as `dtype` (fp32, or rounded to bf16 / fp16). scales and
+ * biases are `scale_dtype` (bf16, fp16 or fp32). out has row stride ldo (ldo % 8 == 0, 16-byte
+ * aligned). A GEMM over `out` then serves wide (prefill) forwards. Replaces the
+ * mx.dequantize(w, scales, biases) of the reference's wide path (wide_gemm.py:173-232).
+ */
+int dspark_qmm_dequantize(const uint32_t* w, const void* scales, const void* biases, int scale_dtype, int64_t N,
+                          int64_t K, int bits, int group_size, int dtype, void* out, int64_t ldo,
+                          dspark_stream stream);
 
 /* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size, M and K
  * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,

@@ -26,6 +26,7 @@
 //     are staged once in LDS and shared by the 4 waves (dspark_qmm_splitk.h). Slices of a
 //     strip are summed by the last workgroup to arrive, in slice order: deterministic and
 //     independent of M. The slice count depends only on the strips and K.
+#include <algorithm>
 #include <mutex>
 
 #include "dspark_qmm_splitk.h"
@@ -494,6 +495,116 @@ extern "C" int dspark_qmm_affine(const void* x, int64_t ldx, int64_t M, int64_t 
                                  void* y, int64_t ldy, void* workspace, size_t workspace_bytes, dspark_stream stream) {
   dspark_qmm_problem p{x, ldx, w, scales, biases, y, ldy, N, K};
   return dspark_qmm_affine_multi(&p, 1, M, bits, group_size, workspace, workspace_bytes, stream);
+}
+
+// ---- dequantize once (the prefill wide path): w [N, K*bits/32] + scales/biases [N, K/64] ->
+// out [N, K], out[n, j] = (scale * q) + bias in fp32 -- a product rounded, then a sum rounded,
+// with no fma contraction, the arithmetic of an elementwise multiply followed by an add --
+// stored as fp32 or rounded once more to bf16 / fp16. Thread = 8 consecutive values of a
+// row (one word of 4-bit fields, two of 8-bit); grid-stride over N*K/8.
+namespace dspark {
+namespace {
+template <int DT>
+__device__ __forceinline__ float load_param(const void* p, long i) {
+  if constexpr (DT == DSPARK_DTYPE_BF16) return bf2f(static_cast<const u16*>(p)[i]);
+  else if constexpr (DT == DSPARK_DTYPE_F16) return (float)__builtin_bit_cast(_Float16, static_cast<const u16*>(p)[i]);
+  else return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ float affine_value(float s, float q, float b) {
+#pragma clang fp contract(off)
+  const float p = s * q;
+  return p + b;
+}
+
+template <int BITS, int SDT, int ODT>
+__global__ __launch_bounds__(256) void dequant_kernel(const u32* __restrict__ w, const void* __restrict__ sc,
+                                                      const void* __restrict__ bi, long N, int K,
+                                                      void* __restrict__ out, long ldo) {
+  const long per_row = K / 8;
+  const long total = N * per_row;
+  for (long c = (long)blockIdx.x * 256 + threadIdx.x; c < total; c += (long)gridDim.x * 256) {
+    const long n = c / per_row;
+    const int j0 = (int)(c - n * per_row) * 8;
+    const long g = n * (K / 64) + j0 / 64;
+    const float s = load_param<SDT>(sc, g), b = load_param<SDT>(bi, g);
+    u32 f[8];
+    if constexpr (BITS == 8) {
+      const u32x2_t wv = ldg64(w + n * (K / 4) + j0 / 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = (wv[i / 4] >> (8 * (i % 4))) & 0xFFu;
+    } else {
+      const u32 wv = w[n * (K / 8) + j0 / 8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = (wv >> (4 * i)) & 0xFu;
+    }
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = affine_value(s, (float)f[i], b);
+    if constexpr (ODT == DSPARK_DTYPE_F32) {
+      float* o = static_cast<float*>(out) + n * ldo + j0;
+      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      u32x4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (ODT == DSPARK_DTYPE_F16) {
+          const _Float16 h0 = (_Float16)v[2 * i], h1 = (_Float16)v[2 * i + 1];
+          o[i] = (u32)__builtin_bit_cast(u16, h0) | ((u32)__builtin_bit_cast(u16, h1) << 16);
+        } else {
+          o[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(static_cast<u16*>(out) + n * ldo + j0) = o;
+    }
+  }
+}
+
+template <int BITS, int SDT>
+void launch_dequant(int odt, unsigned blocks, hipStream_t s, const u32* w, const void* sc, const void* bi, long N,
+                    int K, void* out, long ldo) {
+  if (odt == DSPARK_DTYPE_F32)
+    hipLaunchKernelGGL((dequant_kernel<BITS, SDT, DSPARK_DTYPE_F32>), dim3(blocks), dim3(256), 0, s, w, sc, bi, N, K, out, ldo);
+  else if (odt == DSPARK_DTYPE_F16)
+    hipLaunchKernelGGL((dequant_kernel<BITS, SDT, DSPARK_DTYPE_F16>), dim3(blocks), dim3(256), 0, s, w, sc, bi, N, K, out, ldo);
+  else
+    hipLaunchKernelGGL((dequant_kernel<BITS, SDT, DSPARK_DTYPE_BF16>), dim3(blocks), dim3(256), 0, s, w, sc, bi, N, K, out, ldo);
+}
+
+template <int BITS>
+void launch_dequant_bits(int sdt, int odt, unsigned blocks, hipStream_t s, const u32* w, const void* sc,
+                         const void* bi, long N, int K, void* out, long ldo) {
+  if (sdt == DSPARK_DTYPE_F32) launch_dequant<BITS, DSPARK_DTYPE_F32>(odt, blocks, s, w, sc, bi, N, K, out, ldo);
+  else if (sdt == DSPARK_DTYPE_F16) launch_dequant<BITS, DSPARK_DTYPE_F16>(odt, blocks, s, w, sc, bi, N, K, out, ldo);
+  else launch_dequant<BITS, DSPARK_DTYPE_BF16>(odt, blocks, s, w, sc, bi, N, K, out, ldo);
+}
+
+bool known_dtype(int dt) { return dt == DSPARK_DTYPE_BF16 || dt == DSPARK_DTYPE_F16 || dt == DSPARK_DTYPE_F32; }
+}  // namespace
+}  // namespace dspark
+
+extern "C" int dspark_qmm_dequantize(const uint32_t* w, const void* scales, const void* biases, int scale_dtype,
+                                     int64_t N, int64_t K, int bits, int group_size, int dtype, void* out,
+                                     int64_t ldo, dspark_stream stream) {
+  int st = check_common(1, K, N, bits, group_size);
+  if (st) return st;
+  if (!known_dtype(dtype) || !known_dtype(scale_dtype))
+    return fail(DSPARK_ERR_UNSUPPORTED, "qmm_dequantize: dtype %d / scale dtype %d (bf16, fp16 or fp32)", dtype,
+                scale_dtype);
+  if (!w || !scales || !biases || !out) return fail(DSPARK_ERR_ARG, "qmm_dequantize: null pointer");
+  const int pbytes = scale_dtype == DSPARK_DTYPE_F32 ? 4 : 2;
+  if (!aligned(w, bits == 8 ? 8 : 4) || !aligned(scales, pbytes) || !aligned(biases, pbytes) || !aligned(out, 16) ||
+      ldo % 8)
+    return fail(DSPARK_ERR_ALIGN, "qmm_dequantize: w %d-byte aligned, out 16-byte aligned with ldo %% 8 == 0",
+                bits == 8 ? 8 : 4);
+  if (ldo < K) return fail(DSPARK_ERR_SHAPE, "qmm_dequantize: ldo=%lld < K=%lld", (long long)ldo, (long long)K);
+  const long total = (long)N * (K / 8);
+  const unsigned blocks = (unsigned)std::min<long>((total + 255) / 256, 8192L);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (bits == 8) launch_dequant_bits<8>(scale_dtype, dtype, blocks, s, w, scales, biases, (long)N, (int)K, out, (long)ldo);
+  else launch_dequant_bits<4>(scale_dtype, dtype, blocks, s, w, scales, biases, (long)N, (int)K, out, (long)ldo);
+  return check_launch("dspark_qmm_dequantize");
 }
 
 // ---- split-K counter reset: a fill kernel (not hipMemsetAsync, so the call may sit in a

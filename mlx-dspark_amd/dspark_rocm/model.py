@@ -158,12 +158,19 @@ class DenseModel(nn.Module):
         return [KVCache(1, a.num_key_value_heads, a.head_dim, device=dev, capacity=capacity)
                 for _ in range(a.num_hidden_layers)]
 
-    def forward(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
-        """ids [1, L] -> logits [1, L, V] (the module path)."""
+    def body(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
+        """ids [1, L] -> final-normed hidden states [1, L, H] (the module path)."""
         h = self.embed_tokens[ids]
         for layer, c in zip(self.layers, cache):
             h = layer(h, c)
-        return self.lm_head(rms_norm(h, self.norm, self.args.rms_norm_eps))
+        return rms_norm(h, self.norm, self.args.rms_norm_eps)
+
+    def forward(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
+        """ids [1, L] -> logits [1, L, V] (the module path)."""
+        return self.lm_head(self.body(ids, cache))
+
+
+PREFILL_CHUNK = 2048    # a long prompt prefills in pieces of this many rows (generate.py:1026)
 
 
 class VerifyEngine:
@@ -317,6 +324,28 @@ class Target:
         for c in cache:
             c.advance(M)
         return logits.reshape(1, M, -1), None
+
+    def prefill(self, ids: torch.Tensor, cache: list[KVCache], *, chunk: int | None = None,
+                head_last_row: bool = True) -> torch.Tensor:
+        """Fill the caches with a prompt before the verify loop: module-path forwards of at most
+        ``chunk`` rows (default :data:`PREFILL_CHUNK`), under the prefill wide path the
+        process has configured (``calibrate.apply_wide_gemm``; bit-identical to the stock path
+        by its gate), then the head over the last row only (``head_last_row``) or every row of
+        the final chunk. Returns logits [1, 1 or rows, V] (generate.py:1073-1100,
+        target.py:435-465)."""
+        from . import calibrate
+        from .wide_gemm import wide_matmul
+
+        flat = ids.reshape(1, -1).to(self.model.embed_tokens.device, torch.int64)
+        L = int(flat.shape[1])
+        if L == 0:
+            raise ValueError("prefill: empty prompt")
+        chunk = int(chunk or PREFILL_CHUNK)
+        with wide_matmul(calibrate.WIDE_GEMM_MIN_ROWS, calibrate.WIDE_GEMM_SHAPES):
+            hn = None
+            for i in range(0, L, chunk):
+                hn = self.model.body(flat[:, i:i + chunk], cache)
+            return self.model.lm_head(hn[:, -1:] if head_last_row else hn)
 
     def plain(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
         return self.verify(ids, cache)[0]

@@ -258,6 +258,32 @@ def quantized_swiglu_packed(x: torch.Tensor, pair: PackedSwiGLU, *, group_size: 
     return h.reshape(*x.shape[:-1], pair.n)
 
 
+DEQUANT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}   # dspark_dtype codes
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, bits: int,
+               group_size: int = GROUP, dtype: torch.dtype = torch.float32,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Packed affine ``w [N, K*bits/32]`` -> ``[N, K]`` in ``dtype`` in one launch
+    (``dspark_qmm_dequantize``): ``(scale * q) + bias`` as an fp32 product rounded, then an fp32
+    sum rounded, then rounded to ``dtype``; for fp32 these are the bits of
+    :func:`dspark_rocm.quant.dequantize` (the reference's ``mx.dequantize``, wide_gemm.py:222)."""
+    _require_cuda(w, scales, biases)
+    _require_packed(w)
+    _rowmajor("w", w)
+    if scales.dtype not in DEQUANT_DTYPES or biases.dtype != scales.dtype or dtype not in DEQUANT_DTYPES:
+        raise TypeError(f"dequantize: scales/biases {scales.dtype}/{biases.dtype}, out {dtype}")
+    n, k = int(w.shape[0]), int(w.shape[1]) * 32 // bits
+    scales, biases = scales.contiguous(), biases.contiguous()
+    if out is None:
+        out = torch.empty((n, k), dtype=dtype, device=w.device)
+    elif out.dtype != dtype or tuple(out.shape) != (n, k) or out.stride(-1) != 1:
+        raise ValueError(f"dequantize: out must be [{n}, {k}] {dtype} with unit inner stride")
+    _lib.call("dspark_qmm_dequantize", _ptr(w), _ptr(scales), _ptr(biases), DEQUANT_DTYPES[scales.dtype], n, k,
+              bits, group_size, DEQUANT_DTYPES[dtype], _ptr(out), out.stride(0), _stream(out))
+    return out
+
+
 def qmm_supported(m: int, k: int, n: int, bits: int, group_size: int = GROUP) -> bool:
     return _lib.load().dspark_qmm_affine_supported(m, k, n, bits, group_size) == 0
 
