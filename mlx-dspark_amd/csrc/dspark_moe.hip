@@ -74,13 +74,11 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
   extern __shared__ int lds[];
   int* pair_e = lds;                                                 // [M*k]
   int* counts = lds + a.M * a.k;                                     // [kRouteThreads]
-  u32* tmask = reinterpret_cast<u32*>(counts + kRouteThreads);       // [2][kRouteThreads] token bits (M <= 64)
+  u32* tmask = reinterpret_cast<u32*>(counts + kRouteThreads);       // [2][kRouteThreads] bits of 64 tokens
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int P = a.M * a.k;
 
   counts[threadIdx.x] = 0;
-  tmask[threadIdx.x] = 0;
-  tmask[kRouteThreads + threadIdx.x] = 0;
 
   for (int t = wave; t < a.M; t += kRouteThreads / 64) {
     float xv[NPL];
@@ -139,16 +137,12 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
   if (!a.offsets) return;
   // ---- bucket the (token, slot) pairs by expert, stable in pair id. A token selects an
   // expert at most once, so a pair's place in its bucket is the number of earlier tokens that
-  // selected the same expert.
+  // selected the same expert. Bucket sizes first (order-free), then an exclusive scan, then
+  // the tokens in chunks of 64: one bit per (expert, token of the chunk) gives each pair its
+  // rank among the chunk's earlier tokens, and a running per-expert total carries the
+  // earlier chunks. Cost: M/64 chunks of four barriers, whatever M is.
   __syncthreads();
-  const bool bits = a.M <= 64;
-  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
-    const int pe = pair_e[p], t = p / a.k;
-    if (bits) atomicOr(&tmask[(t >> 5) * kRouteThreads + pe], 1u << (t & 31));
-    else atomicAdd(&counts[pe], 1);
-  }
-  __syncthreads();
-  if (bits) counts[threadIdx.x] = __builtin_popcount(tmask[threadIdx.x]) + __builtin_popcount(tmask[kRouteThreads + threadIdx.x]);
+  for (int p = threadIdx.x; p < P; p += kRouteThreads) atomicAdd(&counts[pair_e[p]], 1);
   __syncthreads();
   // exclusive scan of the bucket sizes by wave 0, 64 experts at a time; counts[e] becomes the
   // bucket start
@@ -171,20 +165,27 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const RouteArg
     }
     if (lane == 0) a.offsets[a.E] = carry;
   }
-  __syncthreads();
-  for (int p = threadIdx.x; p < P; p += kRouteThreads) {
-    const int pe = pair_e[p], t = p / a.k;
-    int before = 0;
-    if (bits) {
-      const u32 lo = tmask[pe], hi = tmask[kRouteThreads + pe];
-      before = (t < 32) ? __builtin_popcount(lo & ((1u << t) - 1u))
-                        : __builtin_popcount(lo) + __builtin_popcount(hi & ((1u << (t - 32)) - 1u));
-    } else {
-      for (int p2 = 0; p2 < p; ++p2) before += (pair_e[p2] == pe);
+  for (int t0 = 0; t0 < a.M; t0 += 64) {
+    tmask[threadIdx.x] = 0;
+    tmask[kRouteThreads + threadIdx.x] = 0;
+    __syncthreads();  // also orders the scan's counts before the first chunk's reads
+    const int q0 = t0 * a.k, q1 = min(t0 + 64, a.M) * a.k;
+    for (int p = q0 + threadIdx.x; p < q1; p += kRouteThreads) {
+      const int tl = p / a.k - t0;
+      atomicOr(&tmask[(tl >> 5) * kRouteThreads + pair_e[p]], 1u << (tl & 31));
     }
-    const int slot = counts[pe] + before;  // bucket start + earlier pairs
-    if (a.sorted) a.sorted[slot] = p;
-    if (a.pos) a.pos[p] = slot;
+    __syncthreads();
+    for (int p = q0 + threadIdx.x; p < q1; p += kRouteThreads) {
+      const int pe = pair_e[p], tl = p / a.k - t0;
+      const u32 lo = tmask[pe], hi = tmask[kRouteThreads + pe];
+      const int before = (tl < 32) ? __builtin_popcount(lo & ((1u << tl) - 1u))
+                                   : __builtin_popcount(lo) + __builtin_popcount(hi & ((1u << (tl - 32)) - 1u));
+      const int slot = counts[pe] + before;  // bucket start + earlier chunks + earlier tokens here
+      if (a.sorted) a.sorted[slot] = p;
+      if (a.pos) a.pos[p] = slot;
+    }
+    __syncthreads();
+    counts[threadIdx.x] += __builtin_popcount(tmask[threadIdx.x]) + __builtin_popcount(tmask[kRouteThreads + threadIdx.x]);
   }
 }
 

@@ -27,7 +27,8 @@ def _logits_with_ties(r, M, E):
     return x
 
 
-@pytest.mark.parametrize("M,E,k", [(16, 128, 8), (1, 128, 8), (4, 64, 4), (16, 256, 8), (33, 128, 2)])
+@pytest.mark.parametrize("M,E,k", [(16, 128, 8), (1, 128, 8), (4, 64, 4), (16, 256, 8), (33, 128, 2),
+                                   (65, 128, 8), (200, 64, 4), (1024, 128, 8), (97, 512, 3), (256, 1024, 32)])
 def test_route_bit_exact(dev, M, E, k):
     import torch
 
