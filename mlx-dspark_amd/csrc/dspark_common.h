@@ -54,6 +54,15 @@ __device__ __forceinline__ u32x4_t ldg128(const void* p) {
 __device__ __forceinline__ u32x2_t ldg64(const void* p) {
   return *reinterpret_cast<const u32x2_t*>(p);
 }
+// Streamed-once data (weights, K/V tiles): the non-temporal hint ("nt") marks the lines for
+// early eviction, so a stream that is read once does not push reused lines out of L2 / MALL.
+// A read-only probe of 108 MB in one launch streams 6.4 TB/s with it and 6.1 TB/s without.
+__device__ __forceinline__ u32x4_t ldg128_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+__device__ __forceinline__ u32x2_t ldg64_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+}
 
 // Wave64 cross-lane exchange (ds_bpermute, no LDS storage).
 __device__ __forceinline__ float shfl_xor(float v, int mask) {

@@ -105,11 +105,11 @@ struct WSlice {
       for (int j = 0; j < KSMAX / 2; ++j) {
         const int g = gs + 2 * min(j, pairs - 1);
         const int qq = (g + 1 < G) ? q : (q & 1);  // no second group at the row end: re-read the first
-        v[j] = ldg128(wrow + 8 * g + 4 * qq);
+        v[j] = ldg128_nt(wrow + 8 * g + 4 * qq);
       }
     } else {
 #pragma unroll
-      for (int gl = 0; gl < KSMAX; ++gl) v[gl] = ldg128(wrow + 16 * (gs + min(gl, gcount - 1)) + 4 * q);
+      for (int gl = 0; gl < KSMAX; ++gl) v[gl] = ldg128_nt(wrow + 16 * (gs + min(gl, gcount - 1)) + 4 * q);
     }
   }
 };
@@ -242,8 +242,8 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     for (int j = 0; j < KSMAX / 8; ++j) {
       const int jj = min(j, (gcount >> 3) - 1);
       const u16* blk = P.s + ((tile16 * (G >> 3) + (gs >> 3) + jj) * 2) * 128 + 8 * c16;
-      tsv[j] = ldg128(blk);
-      tbv[j] = ldg128(blk + 128);
+      tsv[j] = ldg128_nt(blk);
+      tbv[j] = ldg128_nt(blk + 128);
     }
   } else if constexpr (SBVEC) {
 #pragma unroll
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(64 * NS) void qmm_sk_kernel(const QmmSkArgs args) {
     const int nl = BITS == 4 ? (gcount >> 1) : gcount;
     const char* tb = reinterpret_cast<const char*>(P.w) + ((tile16 * per_tile + first) * 64 + lane) * 16;
 #pragma unroll
-    for (int j = 0; j < NL; ++j) wsl.v[j] = ldg128(tb + (long)min(j, nl - 1) * 1024);
+    for (int j = 0; j < NL; ++j) wsl.v[j] = ldg128_nt(tb + (long)min(j, nl - 1) * 1024);
   } else {
     wsl.load(P.w + (long)n * (K * BITS / 32), q, gs, gcount, G);
   }
