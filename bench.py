@@ -139,10 +139,13 @@ def time_eager(fn, repeats: int = REPEATS, warm: int = 2) -> float:
 # ------------------------------------------------------------------ bandwidth
 
 def measure_bandwidth(dev) -> dict:
-    """Achievable HBM bandwidth three ways, median of REPEATS eager calls each: a 1 GiB device
-    copy (read + write bytes), an fp16 matvec streaming a 512 MB matrix (the reference's probe,
-    calibrate.py:871-894) and a plain reduction reading 1 GiB."""
+    """Achievable HBM bandwidth, median of REPEATS eager calls each: a 1 GiB device copy (read +
+    write bytes), the library's streaming-read probe (``dspark_stream_read``, 16-byte
+    non-temporal loads) over 1 GiB and over 108 MB (one gate+up launch's bytes), and an fp16
+    matvec streaming a 512 MB matrix (the reference's probe, calibrate.py:871-894)."""
     import torch
+
+    from dspark_rocm import ops
 
     out = {}
     n = 1 << 30
@@ -150,10 +153,22 @@ def measure_bandwidth(dev) -> dict:
     b = torch.empty_like(a)
     ms = time_eager(lambda: b.copy_(a))
     out["copy_GBs"] = round(2 * n / (ms * 1e-3) / 1e9, 1)
-    x = a.view(torch.bfloat16)
-    ms = time_eager(lambda: torch.sum(x, dtype=torch.float32))
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    ms = time_eager(lambda: ops.stream_read(a, sink))
     out["read_GBs"] = round(n / (ms * 1e-3) / 1e9, 1)
-    del a, b, x
+    # 108 MB at a time, rotating over the 9 disjoint slices of the 1 GiB buffer (more than the
+    # 256 MB MALL), so no call reads from the last one's cache
+    m = 107872256
+    slices = [a[i * m:(i + 1) * m] for i in range(n // m)]
+    chain = 2 * len(slices)
+
+    def reads():
+        for i in range(chain):
+            ops.stream_read(slices[i % len(slices)], sink)
+
+    ms = time_eager(reads) / chain  # back to back, as the qmm legs are timed
+    out["read_108MB_GBs"] = round(m / (ms * 1e-3) / 1e9, 1)
+    del a, b, slices
     dim = int(((512 << 20) / 2) ** 0.5) // 64 * 64
     g = torch.Generator(device=dev)
     g.manual_seed(0)
@@ -374,6 +389,45 @@ def verify_step_bytes(context: int, rows: int) -> tuple[int, int]:
     return weights, kv
 
 
+def bench_prefill_wide(dev, n: int = 12288, k: int = 4096, bits: int = 8, widths=(256, 512, 1024, 2048)) -> dict:
+    """The prefill wide path on the 8B-shaped gate projection ([12288, 4096] 8-bit): per width M,
+    the stock path (torch dequantize + fp32 GEMM), the wide path (one dequantize launch + the same
+    fp32 GEMM, bit-identical) and its bf16 variant (dequantize to bf16 + bf16 GEMM), each called
+    eagerly back to back over 4 distinct matrices (as a prefill runs them); and the dequantize
+    kernel alone, graph-replayed (bytes: the packed weight, scales and biases read, the fp32
+    weight written)."""
+    import torch
+
+    from dspark_rocm import ops, wide_gemm
+    from dspark_rocm.nn import QuantizedLinear
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    mats = [QuantizedLinear.random(n, k, bits=bits, device=dev, generator=g) for _ in range(4)]
+    out = {"shape": f"{n}x{k}", "bits": bits, "widths": []}
+    for M in widths:
+        x = torch.randn((M, k), generator=g, device=dev).to(torch.bfloat16)
+        row = {"M": M}
+        for name, fn in (("stock_us", lambda m: wide_gemm._orig_call(m, x)),
+                         ("wide_us", lambda m: wide_gemm.wide_rows(m, x, exact=True)),
+                         ("wide_bf16_us", lambda m: wide_gemm.wide_rows(m, x, exact=False))):
+            ms = time_eager(lambda: [fn(m) for m in mats]) / len(mats)
+            row[name] = round(ms * 1e3, 1)
+        row["speedup"] = round(row["stock_us"] / row["wide_us"], 2)
+        row["speedup_bf16"] = round(row["stock_us"] / row["wide_bf16_us"], 2)
+        row["bf16_TFLOPs"] = round(2 * M * n * k / (row["wide_bf16_us"] * 1e-6) / 1e12, 1)
+        out["widths"].append(row)
+    nbytes = n * k * bits // 8 + 4 * n * (k // 64) + 4 * n * k
+    outs = [torch.empty((n, k), dtype=torch.float32, device=dev) for _ in mats]
+    ms, _ = time_graph(lambda: [ops.dequantize(m.weight, m.scales, m.biases, bits=bits, out=o)
+                                for m, o in zip(mats, outs)])
+    ms /= len(mats)
+    out["dequantize_us"] = round(ms * 1e3, 2)
+    out["dequantize_bytes"] = nbytes
+    out["dequantize_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    return out
+
+
 def bench_verify_forward(dev, context: int = 16384, rows: int = 16, widths=(1, 2, 4, 8, 16), shallow: int = 512):
     """Speculative verify steps of a random-init dense 8-bit 64-layer target (hidden 5120, heads
     64/8 x 128, intermediate 25600, vocab 151936, RoPE 1e6) over a synthetic bf16 KV cache:
@@ -591,6 +645,7 @@ ONLY = {
     "attn32k_kv4": lambda dev: bench_attention(dev, 32768, kv_bits=4),
     "moe": lambda dev: bench_moe(dev),
     "verify_step": lambda dev: bench_verify_forward(dev, widths=(16,)),
+    "prefill_wide": lambda dev: bench_prefill_wide(dev),
 }
 
 
@@ -726,6 +781,12 @@ def main() -> None:
         legs["moe_block"] = leg("MoE block, 128 experts top-8, 2048/768 4-bit, 16 tokens", r["bytes"], r["us_chained"],
                                 mbw, r["flops"], distinct_experts=r["distinct_experts"])
         log(f"MoE block: {r['us_chained']} us ({r['GBs_chained']} GB/s), {r['distinct_experts']} experts")
+        r = bench_prefill_wide(dev)
+        extra["prefill_wide"] = r
+        legs["prefill_dequantize"] = leg("prefill wide path: dequantize [12288, 4096] 8-bit to fp32 once",
+                                         r["dequantize_bytes"], r["dequantize_us"], mbw)
+        log(f"prefill wide path: {[(w['M'], w['stock_us'], w['wide_us'], w['wide_bf16_us']) for w in r['widths']]}, "
+            f"dequantize {r['dequantize_us']} us ({r['dequantize_GBs']} GB/s)")
         if not a.no_verify_step:
             r = bench_verify_forward(dev)
             extra["verify_step"] = r

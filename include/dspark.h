@@ -135,6 +135,15 @@ int dspark_qmm_dequantize(const uint32_t* w, const void* scales, const void* bia
                           int64_t K, int bits, int group_size, int dtype, void* out, int64_t ldo,
                           dspark_stream stream);
 
+/*
+ * Streaming-read bandwidth probe: reads `bytes` (a positive multiple of 16, 16-byte aligned) once
+ * with 16-byte non-temporal loads; sink[0] is written only in the (practically impossible) case
+ * that the XOR of all words equals a sentinel. Timed by the caller, it gives the measured HBM
+ * read rate the roofline fractions are also quoted against. Replaces the reference's
+ * bandwidth probe (calibrate.py:871-894, an fp16 matvec over 512 MB).
+ */
+int dspark_stream_read(const void* p, size_t bytes, uint32_t* sink, dspark_stream stream);
+
 /* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size, M and K
  * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,
  * biases and y. Replaces the per-projection QuantizedLinear calls of one decoder layer

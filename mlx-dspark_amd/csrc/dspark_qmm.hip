@@ -600,7 +600,7 @@ extern "C" int dspark_qmm_dequantize(const uint32_t* w, const void* scales, cons
                 bits == 8 ? 8 : 4);
   if (ldo < K) return fail(DSPARK_ERR_SHAPE, "qmm_dequantize: ldo=%lld < K=%lld", (long long)ldo, (long long)K);
   const long total = (long)N * (K / 8);
-  const unsigned blocks = (unsigned)std::min<long>((total + 255) / 256, 8192L);
+  const unsigned blocks = (unsigned)std::min<long>((total + 255) / 256, 1L << 20);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (bits == 8) launch_dequant_bits<8>(scale_dtype, dtype, blocks, s, w, scales, biases, (long)N, (int)K, out, (long)ldo);
   else launch_dequant_bits<4>(scale_dtype, dtype, blocks, s, w, scales, biases, (long)N, (int)K, out, (long)ldo);

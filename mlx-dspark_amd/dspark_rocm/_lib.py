@@ -86,6 +86,7 @@ SIGNATURES: dict[str, tuple] = {
                                   c_int, c_int, c_void_p, c_i64, c_void_p, c_size_t, c_void_p]),
     "dspark_qmm_affine_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_int, c_int]),
     "dspark_qmm_workspace_reset": (c_int, [c_void_p, c_size_t, c_void_p]),
+    "dspark_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "dspark_qmm_dequantize": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_i64, c_i64, c_int, c_int, c_int,
                                       c_void_p, c_i64, c_void_p]),
     "dspark_qmm_affine_noalloc": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_i64,

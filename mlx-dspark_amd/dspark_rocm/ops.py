@@ -284,6 +284,15 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, b
     return out
 
 
+def stream_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    """Read every byte of ``buf`` once on the gfx950 streaming-read probe (``dspark_stream_read``);
+    ``sink`` is an int32 scalar tensor the kernel practically never writes. For timing."""
+    _require_cuda(buf, sink)
+    if not buf.is_contiguous():
+        raise ValueError("stream_read: contiguous buffer")
+    _lib.call("dspark_stream_read", _ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream(buf))
+
+
 def qmm_supported(m: int, k: int, n: int, bits: int, group_size: int = GROUP) -> bool:
     return _lib.load().dspark_qmm_affine_supported(m, k, n, bits, group_size) == 0
 

@@ -184,3 +184,19 @@ def test_workspace_reset_restores_counters(dev):
     ops.quantized_matmul_multi([xd], [wd], [sd], [bd], bits=8, outs=[y], workspace=ws)
     assert torch.equal(y, want)
     assert not ws[: 256 << 10].any()               # and the call leaves them at zero
+
+
+def test_stream_read_probe(dev):
+    """The bandwidth probe reads without writing its sink (the fold never equals the sentinel
+    on these bytes) and refuses sizes that are not whole 16-byte chunks."""
+    import torch
+
+    from dspark_rocm import _lib, ops
+
+    buf = torch.arange(1 << 20, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.stream_read(buf, sink)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    with pytest.raises(_lib.DsparkError):
+        _lib.call("dspark_stream_read", buf.data_ptr(), 20, sink.data_ptr(), 0)
