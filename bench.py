@@ -14,9 +14,11 @@ launch stream). ``legs`` carries the same block for each part of the metric: tha
 single 4096x4096 qmm, verify attention at 32k keys (bf16, fp16, head dim 256, 8- and 4-bit KV),
 the MoE block and the 64-layer verify step at 16k context, each with its fraction of the
 8 TB/s peak, of a measured bandwidth (``bandwidth``: the best of a device copy, an fp16 matvec
-over 512 MB as the reference measures it, calibrate.py:871-894, and a plain read) and, where
+over 512 MB as the reference measures it, calibrate.py:871-894, and the library's streaming
+read probe over 1 GiB; the probe over one gate+up launch's 108 MB is reported beside it) and, where
 MFMA does the work, the useful FLOP/s as a fraction of the 2.5 PFLOP/s dense bf16 peak.
-``extra`` holds the sweeps (qmm M, attention L, verify width x depth). ``cpu_baseline``: the C
+``extra`` holds the sweeps (qmm M, attention L, verify width x depth) and the prefill wide path
+(stock vs wide at M 256..2048, and its dequantize kernel, also a leg). ``cpu_baseline``: the C
 restatement (oracle/dspark_oracle.c, OpenMP on every core of this process's affinity) on a
 bounded sample of the layer set, with torch-CPU fp32 and C attention / MoE legs beside it.
 
