@@ -292,8 +292,9 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   // V: thread (key quad vkq = tid % VQ, d-chunk vdc = tid / VQ) loads keys 4vkq..4vkq+3 and
   //    writes the transposed tile as 8 ds_write_b64 (4 keys of one d each); odd d-chunks walk
   //    their 8 d-rows in pair-swapped order so each half-wave covers all 64 LDS banks.
-  // Quantized: K word chunk c = tid + THREADS*j -> (key c / QCH, chunk c % QCH) with the
-  //    scale and bias of its group; V as above with the 8 (or 4) bytes of each key's d-chunk.
+  // Quantized: K word chunk c = tid + THREADS*j -> (key c / QCH, chunk c % QCH); V as above
+  //    with the 8 (or 4) bytes of each key's d-chunk; thread tid < KT reads key tid's scales
+  //    and biases of K and V into the tile's fp32 tables.
   const bool vthread = tid < VQ * DC;
   const int vkq = tid % VQ, vdc = tid / VQ;
   const u16* kbase16 = static_cast<const u16*>(a.k) + b * a.ksb + hk * a.ksh;
@@ -302,9 +303,9 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   const u32* vbase32 = static_cast<const u32*>(a.v) + b * a.vsb + hk * a.vsh;
   struct TileRegs {
     u32x4_t k[QB ? QLOADS : LOADS];
-    u32 ksb[QB ? QLOADS : 1];   // quantized: scale | bias << 16 of each K chunk's group
     u32x4_t v[4];               // plain: 8 T of each key; quantized: words in .x (.y for 8-bit)
-    u32 vsb[QB ? 4 : 1];
+    u32 sb[QB ? 4 * G : 1];     // quantized, threads tid < KT: key tid's K scales, K biases, V
+                                // scales, V biases (G each, T bits)
   };
   // A tile inside the cache is addressed as a uniform base (scalar) plus a loop-invariant
   // 32-bit lane offset; only a tile running past key L - 1 clamps each key.
@@ -339,19 +340,13 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
     }
   };
   auto load_quant = [&](TileRegs& r, int kt) {
-    const u16* ksc = a.ks + b * a.qksb + hk * a.qksh;
-    const u16* kbi = a.kb + b * a.qksb + hk * a.qksh;
 #pragma unroll
     for (int j = 0; j < QLOADS; ++j) {
       const int c = min(tid + THREADS * j, KT * QCH - 1);
       const int key = min(kt + c / QCH, L - 1), ch = c % QCH;
       r.k[j] = ldg128(kbase32 + (long)key * a.kss + 4 * ch);
-      const long gi = (long)key * a.qkss + (ch * QV) / 64;
-      r.ksb[j] = (u32)ksc[gi] | ((u32)kbi[gi] << 16);
     }
     if (vthread) {
-      const u16* vsc = a.vs + b * a.qvsb + hk * a.qvsh;
-      const u16* vbi = a.vb + b * a.qvsb + hk * a.qvsh;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = min(kt + 4 * vkq + j, L - 1);
@@ -362,8 +357,20 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
         } else {
           r.v[j] = u32x4_t{*w, 0u, 0u, 0u};
         }
-        const long gi = (long)key * a.qvss + (8 * vdc) / 64;
-        r.vsb[j] = (u32)vsc[gi] | ((u32)vbi[gi] << 16);
+      }
+    }
+    // the tile's scales and biases: one thread per key reads its 4 G values (a few gathers in
+    // one wave instead of two per chunk in every thread)
+    if (tid < KT) {
+      const int key = min(kt + tid, L - 1);
+      const long ko = b * a.qksb + hk * a.qksh + (long)key * a.qkss;
+      const long vo = b * a.qvsb + hk * a.qvsh + (long)key * a.qvss;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        r.sb[g] = a.ks[ko + g];
+        r.sb[G + g] = a.kb[ko + g];
+        r.sb[2 * G + g] = a.vs[vo + g];
+        r.sb[3 * G + g] = a.vb[vo + g];
       }
     }
   };
@@ -392,12 +399,13 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
             fields8<QB>(w, 8 * e, f);
             *reinterpret_cast<u32x4_t*>(&ks_lds[key * KP + ch * QV + 8 * e]) = fields_to_t<T>(f);
           }
-          if ((ch * QV) % 64 == 0) {  // the chunk that opens a group records its scale and bias
-            const int g = (ch * QV) / 64;
-            qsb[bsel][0][g][key] = to_f32<T>(r.ksb[j] & 0xFFFFu);
-            qsb[bsel][1][g][key] = to_f32<T>(r.ksb[j] >> 16);
-          }
         }
+      }
+      if (tid < KT) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int g = 0; g < G; ++g) qsb[bsel][t][g][tid] = to_f32<T>(r.sb[t * G + g]);
       }
     } else {
 #pragma unroll
@@ -415,14 +423,6 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
           u32 f[8];
           fields8<QB>(w, 0, f);
           vv[j] = fields_to_t<T>(f);
-        }
-        if (vdc % 8 == 0) {  // the d-chunk that opens a group records its keys' scales and biases
-          const int g = vdc / 8;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            qsb[bsel][2][g][4 * vkq + j] = to_f32<T>(r.vsb[j] & 0xFFFFu);
-            qsb[bsel][3][g][4 * vkq + j] = to_f32<T>(r.vsb[j] >> 16);
-          }
         }
       } else {
 #pragma unroll
