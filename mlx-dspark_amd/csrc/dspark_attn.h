@@ -33,7 +33,7 @@
 //     bf16/fp16 cache of the dequantized values.
 #pragma once
 
-#include "dspark_common.h"
+#include "dspark_qmm_core.h"
 
 namespace dspark {
 namespace attn {
@@ -201,6 +201,21 @@ __device__ __forceinline__ void fields8(const u32* w, int first, u32* out) {
   }
 }
 
+// 4-bit fields of word w as 8 T values off + f, in the order (f0, f4, f1, f5, f2, f6, f3, f7):
+// one v_and_or_b32 per pair (off = 128 for bf16, 0x43004300 being the pair (128, 128); 1024
+// for fp16, 0x64006400); the matching x / q order is perm_x_u4's
+template <class T>
+__device__ __forceinline__ u32x4_t unpack4_off(u32 w) {
+  if constexpr (T::kF16) {
+    const u32 m = 0x000F000Fu, c = 0x64006400u;
+    return u32x4_t{and_or(w, m, c), and_or(w >> 4, m, c), and_or(w >> 8, m, c), and_or(w >> 12, m, c)};
+  } else {
+    return unpack_u4(w);
+  }
+}
+template <class T>
+constexpr float kOff4 = T::kF16 ? 1024.0f : 128.0f;
+
 // ---------------------------------------------------------------- pass 1
 
 // Template parameters: T element type; D head dim (64, 128, 256); TREE ancestry mask; WV row
@@ -265,6 +280,11 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   u32x4_t qf[NDC];
 #pragma unroll
   for (int c = 0; c < NDC; ++c) qf[c] = ldg128(qrow + 32 * c + 8 * q4);
+  if constexpr (QB == 4) {
+    // 4-bit K fields sit in LDS in unpack4_off's order: q follows (its row sums do not change)
+#pragma unroll
+    for (int c = 0; c < NDC; ++c) qf[c] = perm_x_u4(qf[c]);
+  }
   // quantized: per group, the row's sum of q (the bias term of the factored score)
   float qsum[QB ? G : 1];
   if constexpr (QB != 0) {
@@ -395,17 +415,28 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
           const u32 w[4] = {r.k[j].x, r.k[j].y, r.k[j].z, r.k[j].w};
 #pragma unroll
           for (int e = 0; e < QV / 8; ++e) {
-            u32 f[8];
-            fields8<QB>(w, 8 * e, f);
-            *reinterpret_cast<u32x4_t*>(&ks_lds[key * KP + ch * QV + 8 * e]) = fields_to_t<T>(f);
+            u32x4_t val;
+            if constexpr (QB == 4) {
+              val = unpack4_off<T>(w[e]);
+            } else {
+              u32 f[8];
+              fields8<QB>(w, 8 * e, f);
+              val = fields_to_t<T>(f);
+            }
+            *reinterpret_cast<u32x4_t*>(&ks_lds[key * KP + ch * QV + 8 * e]) = val;
           }
         }
       }
       if (tid < KT) {
+        // 4-bit fields are staged as off + f: bias - off * scale takes the offset back out
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; t += 2)
 #pragma unroll
-          for (int g = 0; g < G; ++g) qsb[bsel][t][g][tid] = to_f32<T>(r.sb[t * G + g]);
+          for (int g = 0; g < G; ++g) {
+            const float sc = to_f32<T>(r.sb[t * G + g]), bi = to_f32<T>(r.sb[(t + 1) * G + g]);
+            qsb[bsel][t][g][tid] = sc;
+            qsb[bsel][t + 1][g][tid] = QB == 4 ? __builtin_fmaf(-kOff4<T>, sc, bi) : bi;
+          }
       }
     } else {
 #pragma unroll
@@ -416,7 +447,10 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
     }
     if (vthread) {
       u32x4_t vv[4];
-      if constexpr (QB) {
+      if constexpr (QB == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vv[j] = unpack4_off<T>(r.v[j].x);
+      } else if constexpr (QB == 8) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const u32 w[2] = {r.v[j].x, r.v[j].y};
@@ -429,14 +463,29 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
         for (int j = 0; j < 4; ++j) vv[j] = r.v[j];
       }
       const int pos = vt_pos(4 * vkq);
+      if constexpr (QB == 4) {
+        // word t of vv[j] holds the pair (t, t + 4): odd d-chunks walk their rows in the
+        // half-swapped order e ^ 4, so the word is e & 3 in every lane and only the half differs
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 8 * vdc + (e ^ (vdc & 1));
-        const int wd = e >> 1;
-        const u32 vsel = (e & 1) ? vsel_odd : vsel_even;
-        const u32x2_t pr = {__builtin_amdgcn_perm(vv[1][wd], vv[0][wd], vsel),
-                            __builtin_amdgcn_perm(vv[3][wd], vv[2][wd], vsel)};
-        *reinterpret_cast<u32x2_t*>(&vt_lds[vt_off<KT>(d, pos)]) = pr;
+        for (int e = 0; e < 8; ++e) {
+          const int ep = e ^ (4 * (vdc & 1));
+          const int d = 8 * vdc + ep;
+          const int wd = e & 3;
+          const u32 vsel = (ep >> 2) ? sel_hi : sel_lo;
+          const u32x2_t pr = {__builtin_amdgcn_perm(vv[1][wd], vv[0][wd], vsel),
+                              __builtin_amdgcn_perm(vv[3][wd], vv[2][wd], vsel)};
+          *reinterpret_cast<u32x2_t*>(&vt_lds[vt_off<KT>(d, pos)]) = pr;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = 8 * vdc + (e ^ (vdc & 1));
+          const int wd = e >> 1;
+          const u32 vsel = (e & 1) ? vsel_odd : vsel_even;
+          const u32x2_t pr = {__builtin_amdgcn_perm(vv[1][wd], vv[0][wd], vsel),
+                              __builtin_amdgcn_perm(vv[3][wd], vv[2][wd], vsel)};
+          *reinterpret_cast<u32x2_t*>(&vt_lds[vt_off<KT>(d, pos)]) = pr;
+        }
       }
     }
   };
