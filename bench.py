@@ -500,7 +500,7 @@ def bench_verify_forward(dev, context: int = 16384, rows: int = 16, widths=(1, 2
     res = {"layers": 64, "hidden": 5120, "context": context, "rows": rows, "weight_bytes": weights, "kv_bytes": kv,
            "bytes": by, "ms_graph": round(ms, 4), "GBs": round(by / (ms * 1e-3) / 1e9, 1),
            "frac_of_peak": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "accepted": accepted,
-           "accepted_expected": rows - 1, "draft_passes": passes, "launches": 64 * 10 + 5,
+           "accepted_expected": rows - 1, "draft_passes": passes, "launches": 64 * 9 + 4,
            "build_s": round(build_s, 1),
            "curve": curve, "depth_slope_us_per_token": slope}
     del model, tgt, cache, e

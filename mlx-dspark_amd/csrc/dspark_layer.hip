@@ -284,6 +284,87 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const u16* 
   }
 }
 
+// Argmax of every row and the greedy accept count in one launch: workgroup (c, m) scans chunk c
+// of row m (kAaValues values, every load of a thread issued before any is compared), stores its
+// best (value, index) with device-coherent stores and arrives on a counter; the workgroup that
+// arrives last reduces each row's chunk results (the same strict order, so the same index as
+// argmax_rows_kernel), counts the accepted drafts and clears the counter.
+constexpr int kAaThreads = 256;
+constexpr int kAaLoads = 4;                                  // 16-byte chunks per thread
+constexpr int kAaValues = kAaThreads * kAaLoads * 8;         // values per workgroup
+
+__global__ __launch_bounds__(kAaThreads) void argmax_accept_kernel(const u16* __restrict__ x, long ld, int V,
+                                                                   int M, const int32_t* __restrict__ draft,
+                                                                   int m_draft, int32_t* __restrict__ tt,
+                                                                   int32_t* __restrict__ n_out, int* ctr,
+                                                                   float* pval, int* pidx) {
+  __shared__ float sv[kAaThreads / 64];
+  __shared__ int si[kAaThreads / 64];
+  __shared__ int last;
+  const int C = gridDim.x, c = blockIdx.x, m = blockIdx.y;
+  const u16* row = x + (long)m * ld;
+  const int chunks = V >> 3;
+  const int c0 = c * (kAaValues / 8);
+  float best = -INFINITY;
+  int bid = 0x7FFFFFFF;
+  u32x4_t v[kAaLoads] = {};
+  if (chunks > 0) {  // every load of the thread first (clamped to the row's last whole chunk)
+#pragma unroll
+    for (int u = 0; u < kAaLoads; ++u) v[u] = ldg128(row + 8 * min(c0 + (int)threadIdx.x + u * kAaThreads, chunks - 1));
+  }
+#pragma unroll
+  for (int u = 0; u < kAaLoads; ++u) {
+    const int cc = c0 + (int)threadIdx.x + u * kAaThreads;
+    if (cc < chunks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        arg_better(best, bid, bf2f(v[u][i] & 0xFFFFu), 8 * cc + 2 * i);
+        arg_better(best, bid, bf2f(v[u][i] >> 16), 8 * cc + 2 * i + 1);
+      }
+    }
+  }
+  if (c == C - 1)
+    for (int j = 8 * chunks + threadIdx.x; j < V; j += kAaThreads) arg_better(best, bid, bf2f(row[j]), j);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float v2 = shfl_xor(best, o);
+    const int i2 = __builtin_amdgcn_ds_bpermute((__lane_id() ^ o) << 2, bid);
+    arg_better(best, bid, v2, i2);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = best;
+    si[threadIdx.x >> 6] = bid;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int id = si[0];
+    for (int w = 1; w < kAaThreads / 64; ++w) arg_better(b, id, sv[w], si[w]);
+    __hip_atomic_store(&pval[m * C + c], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&pidx[m * C + c], id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): both stores are complete before the arrival
+    last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == C * M - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  for (int r = threadIdx.x; r < M; r += kAaThreads) {
+    float b = -INFINITY;
+    int id = 0x7FFFFFFF;
+    for (int j = 0; j < C; ++j)
+      arg_better(b, id, __hip_atomic_load(&pval[r * C + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(&pidx[r * C + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    tt[r] = (id == 0x7FFFFFFF) ? 0 : id;  // an all-NaN row reports token 0
+  }
+  __syncthreads();
+  __threadfence_block();
+  if (threadIdx.x == 0) {
+    int n = 0;
+    while (n < m_draft && draft[n] == tt[n]) ++n;
+    n_out[0] = n;
+    __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 __global__ void greedy_accept_kernel(const int32_t* __restrict__ draft, int m, const int32_t* __restrict__ tt,
                                      int32_t* __restrict__ n_out) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
@@ -376,6 +457,38 @@ extern "C" int dspark_argmax_rows(const void* logits, int64_t ld, int64_t M, int
   hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)M), dim3(kArgmaxThreads), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u16*>(logits), (long)ld, (int)V, out);
   return check_launch("argmax_rows");
+}
+
+namespace {
+int aa_chunks(int64_t V) { return (int)((V + kAaValues - 1) / kAaValues); }
+}  // namespace
+
+extern "C" size_t dspark_argmax_accept_workspace(int64_t M, int64_t V) {
+  if (M < 1 || M > 65535 || V < 1 || V >= (1L << 30)) return 0;
+  return 256 + (size_t)M * aa_chunks(V) * 8;
+}
+
+extern "C" int dspark_argmax_accept(const void* logits, int64_t ld, int64_t M, int64_t V, const int32_t* draft,
+                                    int64_t m_draft, int32_t* target_tokens, int32_t* n_accepted, void* workspace,
+                                    size_t workspace_bytes, dspark_stream stream) {
+  if (!logits || !target_tokens || !n_accepted || (m_draft > 0 && !draft) || !workspace)
+    return fail(DSPARK_ERR_ARG, "argmax_accept: null pointer");
+  if (M < 1 || M > 65535 || V < 1 || V >= (1L << 30) || ld < V || m_draft < 0 || m_draft > M)
+    return fail(DSPARK_ERR_SHAPE, "argmax_accept: M=%lld V=%lld m_draft=%lld", (long long)M, (long long)V,
+                (long long)m_draft);
+  if (!aligned(logits, 16) || ld % 8) return fail(DSPARK_ERR_ALIGN, "argmax_accept: rows must be 16-byte aligned (ld %% 8 == 0)");
+  const size_t need = dspark_argmax_accept_workspace(M, V);
+  if (workspace_bytes < need)
+    return fail(DSPARK_ERR_WORKSPACE, "argmax_accept: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (!aligned(workspace, 256)) return fail(DSPARK_ERR_ALIGN, "argmax_accept: workspace must be 256-byte aligned");
+  const int C = aa_chunks(V);
+  char* ws = static_cast<char*>(workspace);
+  float* pval = reinterpret_cast<float*>(ws + 256);
+  int* pidx = reinterpret_cast<int*>(ws + 256 + (size_t)M * C * 4);
+  hipLaunchKernelGGL(argmax_accept_kernel, dim3((unsigned)C, (unsigned)M), dim3(kAaThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u16*>(logits), (long)ld, (int)V, (int)M,
+                     draft, (int)m_draft, target_tokens, n_accepted, reinterpret_cast<int*>(ws), pval, pidx);
+  return check_launch("argmax_accept");
 }
 
 extern "C" int dspark_greedy_accept(const int32_t* draft, int64_t m, const int32_t* target_tokens, int32_t* n_accepted,

@@ -144,6 +144,9 @@ SIGNATURES: dict[str, tuple] = {
     "dspark_swiglu": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p]),
     "dspark_argmax_rows": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p]),
     "dspark_greedy_accept": (c_int, [c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),
+    "dspark_argmax_accept_workspace": (c_size_t, [c_i64, c_i64]),
+    "dspark_argmax_accept": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p, c_void_p, c_void_p,
+                                     c_size_t, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -16,7 +16,7 @@ Two forwards of the same weights live here:
   one q/k/v qmm launch, one q/k-norm + RoPE + cache-write kernel, split-KV attention writing
   o_proj's input rows directly, the o qmm, residual-add + RMSNorm, one fused gate/up/SwiGLU
   qmm launch (packed weights; else a gate/up launch and the SwiGLU kernel), the down qmm; then
-  the final norm, lm_head, device argmax and greedy accept. All buffers, the qmm and attention
+  the final norm, lm_head, and the device argmax with greedy accept (one launch). All buffers, the qmm and attention
   workspaces included, are preallocated for up to ``max_rows`` rows and any cache length, so a
   step can be captured in a hipGraph and replayed after steps at other depths.
 
@@ -220,6 +220,8 @@ class VerifyEngine:
         # The engine's own workspaces, sized once for every launch of a step at up to max_rows
         # rows and any cache length, so a captured step never sees them move.
         self.qmm_ws = ops.new_qmm_workspace(dev, self._qmm_workspace_need())
+        self.accept_ws = torch.zeros(max(ops.argmax_accept_workspace_bytes(max_rows, a.vocab_size), 256),
+                                     dtype=torch.uint8, device=dev)
         self.attn_ws = torch.empty(max(ops.attention_workspace_bound(1, hq, hk, d, max_rows), 16), dtype=torch.uint8,
                                    device=dev)
 
@@ -292,8 +294,7 @@ class VerifyEngine:
         logits = self.logits[:M]
         self._qmm(y, [lm], [logits])
         if accept:
-            ops.argmax_rows(logits, out=self.tt[:M])
-            ops.greedy_accept(self.draft[:M - 1], self.tt[:M], out=self.n_acc)
+            ops.argmax_accept(logits, self.draft[:M - 1], self.tt[:M], self.n_acc, self.accept_ws)
         return logits
 
 

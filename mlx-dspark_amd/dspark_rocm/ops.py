@@ -649,3 +649,23 @@ def greedy_accept(draft: torch.Tensor, target_tokens: torch.Tensor, out: torch.T
     d = draft.to(device=target_tokens.device, dtype=torch.int32).contiguous() if m else None
     _lib.call("dspark_greedy_accept", _ptr(d), m, _ptr(target_tokens), _ptr(out), _stream(target_tokens))
     return out
+
+
+def argmax_accept_workspace_bytes(M: int, V: int) -> int:
+    """Workspace bytes of :func:`argmax_accept` for ``M`` rows of ``V`` logits."""
+    return int(_lib.load().dspark_argmax_accept_workspace(M, V))
+
+
+def argmax_accept(logits: torch.Tensor, draft: torch.Tensor, target_tokens: torch.Tensor, n_accepted: torch.Tensor,
+                  workspace: torch.Tensor) -> None:
+    """:func:`argmax_rows` into ``target_tokens`` and :func:`greedy_accept` of ``draft`` into
+    ``n_accepted``, in one launch. ``workspace`` (uint8, >= :func:`argmax_accept_workspace_bytes`,
+    zero-filled when allocated) holds an arrival counter that every call leaves at zero."""
+    _require_cuda(logits, target_tokens, n_accepted, workspace)
+    _require_bf16("logits", logits)
+    M, V = logits.shape
+    m = int(draft.numel())
+    if m and (draft.dtype != torch.int32 or not draft.is_contiguous() or draft.device != logits.device):
+        raise ValueError("argmax_accept: draft must be a contiguous int32 tensor on the logits' device")
+    _lib.call("dspark_argmax_accept", _ptr(logits), logits.stride(0), M, V, _ptr(draft) if m else None, m,
+              _ptr(target_tokens), _ptr(n_accepted), _ptr(workspace), workspace.numel(), _stream(logits))

@@ -75,6 +75,67 @@ def test_qk_norm_rope_kv_kernel(dev, D, Hq, Hk):
     assert not kc[:, :pos0].any() and not kc[:, pos0 + M:].any()   # nothing outside the block
 
 
+def _argmax_ref(rows: np.ndarray) -> list[int]:
+    """First index of the maximum; NaN never chosen (an all-NaN row gives 0)."""
+    out = []
+    for r in rows:
+        r = np.where(np.isnan(r), -np.inf, r)
+        out.append(int(np.argmax(r)))
+    return out
+
+
+@pytest.mark.parametrize("M,V", [(16, 151936), (6, 8192), (3, 8193), (2, 5), (16, 100003), (1, 32000)])
+def test_argmax_accept_fused(dev, M, V):
+    """One launch of argmax + greedy accept equals argmax_rows followed by greedy_accept: ties
+    across the workgroups' chunks go to the first index, NaN is never chosen, the last element
+    and a ragged tail count; repeated calls and graph replays leave the counter at zero."""
+    from dspark_rocm import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(M * 7 + V)
+    ld = (V + 7) // 8 * 8                                           # rows 16-byte aligned, V ragged
+    logits = torch.randn((M, ld), generator=g, device=dev).to(torch.bfloat16)[:, :V]
+    if V > 9000:
+        logits[0, 8200] = 40.0
+        logits[0, V - 3] = 40.0                                     # tie across chunks: 8200 wins
+        logits[M - 1, V - 1] = 45.0                                 # the last element
+    if M > 2:
+        logits[1] = float("nan")                                    # all NaN -> token 0
+        logits[2, : V // 2] = float("nan")                          # NaN never chosen
+        logits[2, V // 2] = 30.0
+    want = _argmax_ref(_np(logits).astype(np.float64))
+    assert ops.argmax_rows(logits).cpu().tolist() == want
+    ws = torch.zeros(ops.argmax_accept_workspace_bytes(M, V), dtype=torch.uint8, device=dev)
+    tt = torch.empty(M, dtype=torch.int32, device=dev)
+    n = torch.empty(1, dtype=torch.int32, device=dev)
+    for k in range(min(M - 1, 3) + 1):                              # drafts matching k leading tokens
+        draft = want[:k] + ([want[k] + 1] if k < M - 1 else [])
+        d = torch.tensor(draft, dtype=torch.int32, device=dev)
+        tt.fill_(-1)
+        ops.argmax_accept(logits, d, tt, n, ws)
+        assert tt.cpu().tolist() == want
+        assert int(n.item()) == verify_ref.greedy_accept(draft, want)[0]
+        assert int(ops.greedy_accept(d, tt).item()) == int(n.item())
+        assert not ws[:256].any()
+    d = torch.tensor(want[: M - 1], dtype=torch.int32, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.argmax_accept(logits, d, tt, n, ws)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        ops.argmax_accept(logits, d, tt, n, ws)
+    for _ in range(3):
+        tt.fill_(-1)
+        n.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert tt.cpu().tolist() == want and int(n.item()) == M - 1
+        assert not ws[:256].any()
+
+
 def test_swiglu_argmax_accept_kernels(dev):
     from dspark_rocm import ops
 
