@@ -420,8 +420,9 @@ int dspark_greedy_accept(const int32_t* draft, int64_t m, const int32_t* target_
 /* The greedy verify round's device part in one launch: target_tokens[m] = argmax over V of
  * logits[m] for m < M (exactly dspark_argmax_rows: first index of the maximum, NaN never chosen)
  * and n_accepted[0] = the number of leading i < m_draft with draft[i] == target_tokens[i]
- * (exactly dspark_greedy_accept). Each row is scanned by ceil(V / 8192) workgroups; the last to
- * finish reduces them and counts. Replaces tt = mx.argmax(v_logits[0], -1) and
+ * (exactly dspark_greedy_accept). Each row is scanned by ceil(V / 16384) workgroups; the last
+ * to finish reduces them and counts (V <= 33554432, m_draft <= 1024). Replaces
+ * tt = mx.argmax(v_logits[0], -1) and
  * n = sum(cumprod(draft == tt)) of the verify loop (generate.py:1544-1555).
  * workspace >= dspark_argmax_accept_workspace(M, V) bytes, 256-byte aligned, its first 256 bytes
  * zero before the first call (an arrival counter; every call leaves it zero). */

@@ -290,8 +290,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const u16* 
 // arrives last reduces each row's chunk results (the same strict order, so the same index as
 // argmax_rows_kernel), counts the accepted drafts and clears the counter.
 constexpr int kAaThreads = 256;
-constexpr int kAaLoads = 4;                                  // 16-byte chunks per thread
+constexpr int kAaLoads = 8;                                  // 16-byte chunks per thread
 constexpr int kAaValues = kAaThreads * kAaLoads * 8;         // values per workgroup
+constexpr int kAaLds = 2048;                                 // chunk results staged per round
+constexpr int kAaDraft = 4;                                  // drafts per thread: m_draft <= 1024
 
 __global__ __launch_bounds__(kAaThreads) void argmax_accept_kernel(const u16* __restrict__ x, long ld, int V,
                                                                    int M, const int32_t* __restrict__ draft,
@@ -301,6 +303,9 @@ __global__ __launch_bounds__(kAaThreads) void argmax_accept_kernel(const u16* __
   __shared__ float sv[kAaThreads / 64];
   __shared__ int si[kAaThreads / 64];
   __shared__ int last;
+  __shared__ float lv[kAaLds];
+  __shared__ int li[kAaLds];
+  __shared__ int ltt[kAaThreads * kAaDraft];
   const int C = gridDim.x, c = blockIdx.x, m = blockIdx.y;
   const u16* row = x + (long)m * ld;
   const int chunks = V >> 3;
@@ -347,20 +352,44 @@ __global__ __launch_bounds__(kAaThreads) void argmax_accept_kernel(const u16* __
   }
   __syncthreads();
   if (!last) return;
-  for (int r = threadIdx.x; r < M; r += kAaThreads) {
-    float b = -INFINITY;
-    int id = 0x7FFFFFFF;
-    for (int j = 0; j < C; ++j)
-      arg_better(b, id, __hip_atomic_load(&pval[r * C + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 __hip_atomic_load(&pidx[r * C + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    tt[r] = (id == 0x7FFFFFFF) ? 0 : id;  // an all-NaN row reports token 0
+  // the drafts are requested now, compared once the tokens are known
+  __shared__ int first_miss;
+  int dv[kAaDraft];
+#pragma unroll
+  for (int u = 0; u < kAaDraft; ++u) {
+    const int i = threadIdx.x + u * kAaThreads;
+    dv[u] = i < m_draft ? draft[i] : 0;
+  }
+  if (threadIdx.x == 0) first_miss = m_draft;
+  // every chunk result of a run of rows into LDS at once (the whole workgroup's loads in flight
+  // together), then one thread per row reduces its chunks in order
+  const int rpc = kAaLds / C;  // >= 1 (C <= kAaLds, checked by the host)
+  for (int r0 = 0; r0 < M; r0 += rpc) {
+    const int ne = min(rpc, M - r0) * C;
+    for (int e = threadIdx.x; e < ne; e += kAaThreads) {
+      lv[e] = __hip_atomic_load(&pval[r0 * C + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      li[e] = __hip_atomic_load(&pidx[r0 * C + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < min(rpc, M - r0); r += kAaThreads) {
+      float b = -INFINITY;
+      int id = 0x7FFFFFFF;
+      for (int j = 0; j < C; ++j) arg_better(b, id, lv[r * C + j], li[r * C + j]);
+      const int tok = (id == 0x7FFFFFFF) ? 0 : id;  // an all-NaN row reports token 0
+      tt[r0 + r] = tok;
+      if (r0 + r < m_draft) ltt[r0 + r] = tok;
+    }
+    __syncthreads();
+  }
+  // accepted = the first i < m_draft with draft[i] != tt[i] (m_draft when none)
+#pragma unroll
+  for (int u = 0; u < kAaDraft; ++u) {
+    const int i = threadIdx.x + u * kAaThreads;
+    if (i < m_draft && dv[u] != ltt[i]) atomicMin(&first_miss, i);
   }
   __syncthreads();
-  __threadfence_block();
   if (threadIdx.x == 0) {
-    int n = 0;
-    while (n < m_draft && draft[n] == tt[n]) ++n;
-    n_out[0] = n;
+    n_out[0] = first_miss;
     __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -464,7 +493,7 @@ int aa_chunks(int64_t V) { return (int)((V + kAaValues - 1) / kAaValues); }
 }  // namespace
 
 extern "C" size_t dspark_argmax_accept_workspace(int64_t M, int64_t V) {
-  if (M < 1 || M > 65535 || V < 1 || V >= (1L << 30)) return 0;
+  if (M < 1 || M > 65535 || V < 1 || V > (int64_t)kAaLds * kAaValues) return 0;
   return 256 + (size_t)M * aa_chunks(V) * 8;
 }
 
@@ -473,7 +502,8 @@ extern "C" int dspark_argmax_accept(const void* logits, int64_t ld, int64_t M, i
                                     size_t workspace_bytes, dspark_stream stream) {
   if (!logits || !target_tokens || !n_accepted || (m_draft > 0 && !draft) || !workspace)
     return fail(DSPARK_ERR_ARG, "argmax_accept: null pointer");
-  if (M < 1 || M > 65535 || V < 1 || V >= (1L << 30) || ld < V || m_draft < 0 || m_draft > M)
+  if (M < 1 || M > 65535 || V < 1 || V > (int64_t)kAaLds * kAaValues || ld < V || m_draft < 0 || m_draft > M ||
+      m_draft > kAaThreads * kAaDraft)
     return fail(DSPARK_ERR_SHAPE, "argmax_accept: M=%lld V=%lld m_draft=%lld", (long long)M, (long long)V,
                 (long long)m_draft);
   if (!aligned(logits, 16) || ld % 8) return fail(DSPARK_ERR_ALIGN, "argmax_accept: rows must be 16-byte aligned (ld %% 8 == 0)");
