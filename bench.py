@@ -357,23 +357,30 @@ def bench_moe(dev, m=16, E=128, k=8, H=2048, I=768, bits=4):
     per_layer = 3 * E * I * H * bits // 8
     pool = max(2, (4 * MALL_BYTES) // per_layer + 1)
     layers = [(stack(I, H), stack(I, H), stack(H, I)) for _ in range(pool)]
+    # the packed expert form (what SwitchGLU.pack() holds for a loaded model), bit-identical
+    packed = [tuple((ops.moe_pack(w, bits=bits), s, b) for (w, s, b) in L) for L in layers]
     x = torch.randn((m, H), generator=g, device=dev).to(torch.bfloat16)
     logits = torch.randn((m, E), generator=g, device=dev).to(torch.bfloat16)
-    _, inds, _ = ops.moe_switch_glu(x, logits, *layers[0], k=k, bits=bits)
+    _, inds, _ = ops.moe_switch_glu(x, logits, *packed[0], k=k, bits=bits)
     distinct = int(torch.unique(inds).numel())
 
-    def chain():
-        for gu in layers:
-            ops.moe_switch_glu(x, logits, *gu, k=k, bits=bits)
+    def chain(ls):
+        def f():
+            for gu in ls:
+                ops.moe_switch_glu(x, logits, *gu, k=k, bits=bits)
+        return f
 
-    ms, _ = time_graph(chain)
+    ms, _ = time_graph(chain(packed))
     us = ms * 1e3 / pool
+    ms_rm, _ = time_graph(chain(layers))
+    us_rm = ms_rm * 1e3 / pool
     per_expert = 3 * (I * H * bits // 8 + 4 * I * (H // 64))
     by = distinct * per_expert + 2 * m * H * 2 + 2 * m * E
-    del layers
+    del layers, packed
     torch.cuda.empty_cache()
     return {"experts": E, "top_k": k, "distinct_experts": distinct, "bytes": by, "us_chained": round(us, 3),
-            "GBs_chained": round(by / us / 1e3, 1), "flops": 3 * 2 * m * k * I * H}
+            "GBs_chained": round(by / us / 1e3, 1), "flops": 3 * 2 * m * k * I * H, "weights": "packed experts",
+            "us_chained_row_major": round(us_rm, 3)}
 
 
 VERIFY_ARGS = dict(hidden_size=5120, num_hidden_layers=64, intermediate_size=25600, num_attention_heads=64,
@@ -782,7 +789,7 @@ def main() -> None:
         extra["moe_block"] = r
         legs["moe_block"] = leg("MoE block, 128 experts top-8, 2048/768 4-bit, 16 tokens", r["bytes"], r["us_chained"],
                                 mbw, r["flops"], distinct_experts=r["distinct_experts"])
-        log(f"MoE block: {r['us_chained']} us ({r['GBs_chained']} GB/s), {r['distinct_experts']} experts")
+        log(f"MoE block: {r['us_chained']} us ({r['GBs_chained']} GB/s, packed experts; row-major {r['us_chained_row_major']} us), {r['distinct_experts']} experts")
         r = bench_prefill_wide(dev)
         extra["prefill_wide"] = r
         legs["prefill_dequantize"] = leg("prefill wide path: dequantize [12288, 4096] 8-bit to fp32 once",

@@ -375,6 +375,29 @@ int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t 
 
 size_t dspark_moe_workspace(int64_t M, int64_t H, int64_t I, int64_t E, int64_t k);
 
+/*
+ * Packed expert weights (no counterpart in the reference, whose experts stay in mlx-lm's
+ * QuantizedSwitchLinear layout): each expert's [N, K] weights in 16-row tiles in the MFMA lane
+ * order, one contiguous 1 KB read per wave per group (8-bit) or group pair (4-bit), experts one
+ * after another (the same bytes as [E, N, K*bits/32]). Scales and biases keep their [E, N, K/64]
+ * layout. Requires N % 16 == 0 and K % 128 == 0. dspark_moe_packed_bytes sizes the buffer (0 =
+ * shape not supported); dspark_moe_pack writes it from the row-major weights (16-byte aligned).
+ */
+size_t dspark_moe_packed_bytes(int64_t E, int64_t N, int64_t K, int bits, int group_size);
+
+int dspark_moe_pack(const uint32_t* w, int64_t E, int64_t N, int64_t K, int bits, int group_size, void* packed,
+                    size_t packed_bytes, dspark_stream stream);
+
+/* dspark_moe_switch_glu with w_gate / w_up / w_down in dspark_moe_pack's form (H and I multiples
+ * of 16, K % 128 == 0 for both projections, 16-byte aligned scales and biases): the same
+ * results, bit for bit. */
+int dspark_moe_switch_glu_packed(const void* x, const void* logits, int64_t M, int64_t H, int64_t I, int64_t E,
+                                 int64_t k, int renorm, const void* w_gate, const void* s_gate, const void* b_gate,
+                                 const void* w_up, const void* s_up, const void* b_up, const void* w_down,
+                                 const void* s_down, const void* b_down, int bits, int group_size, void* out,
+                                 int32_t* inds, void* scores, void* workspace, size_t workspace_bytes,
+                                 dspark_stream stream);
+
 /* ------------------------------------------------------------------ verify-forward layer kernels */
 
 /*

@@ -503,10 +503,10 @@ RcPlan rc_plan(long K, long N, bool swiglu, const void* s, const void* b) {
   return p;
 }
 
-template <bool SWIGLU>
+template <bool SWIGLU, bool PW = false>
 int launch_moe_rc(const MoeRcArgs& a, const RcPlan& p, int E, int bits, hipStream_t s) {
   const dim3 grid((unsigned)p.strips, (unsigned)(E * a.mtiles));
-#define MOE_RC(B, KS, KW) hipLaunchKernelGGL((moe_rc_kernel<B, KS, KW, SWIGLU>), grid, dim3(256), 0, s, a)
+#define MOE_RC(B, KS, KW) hipLaunchKernelGGL((moe_rc_kernel<B, KS, KW, SWIGLU, PW>), grid, dim3(256), 0, s, a)
 #define MOE_RC_KW(B, KS)                                     \
   if (p.kw == 1) MOE_RC(B, KS, 1);                           \
   else if (SWIGLU || p.kw == 2) MOE_RC(B, KS, 2);            \
@@ -596,12 +596,14 @@ extern "C" size_t dspark_moe_workspace(int64_t M, int64_t H, int64_t I, int64_t 
   return moe_layout(M, H, I, E, k, 4).total;
 }
 
-extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t H, int64_t I, int64_t E,
-                                     int64_t k, int renorm, const uint32_t* w_gate, const void* s_gate,
-                                     const void* b_gate, const uint32_t* w_up, const void* s_up, const void* b_up,
-                                     const uint32_t* w_down, const void* s_down, const void* b_down, int bits,
-                                     int group_size, void* out, int32_t* inds, void* scores, void* workspace,
-                                     size_t workspace_bytes, dspark_stream stream) {
+namespace dspark {
+namespace {
+// The fused MoE block over row-major (packed = false) or dspark_moe_pack weights.
+int switch_glu_impl(const void* x, const void* logits, int64_t M, int64_t H, int64_t I, int64_t E, int64_t k,
+                    int renorm, const uint32_t* w_gate, const void* s_gate, const void* b_gate, const uint32_t* w_up,
+                    const void* s_up, const void* b_up, const uint32_t* w_down, const void* s_down,
+                    const void* b_down, int bits, int group_size, void* out, int32_t* inds, void* scores,
+                    void* workspace, size_t workspace_bytes, dspark_stream stream, bool packed) {
   if (!x || !logits || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up || !w_down || !s_down || !b_down || !out)
     return fail(DSPARK_ERR_ARG, "moe_switch_glu: null pointer");
   int st = check_route(M, E, k);
@@ -669,7 +671,14 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   g.mtiles = L.gu.mtiles;
   g.S = L.gu.S;
   const RcPlan rgu = rc_plan(H, I, true, s_gate, b_gate), rgu2 = rc_plan(H, I, true, s_up, b_up);
-  if (rgu.kw && rgu2.kw) {
+  const RcPlan rdn = rc_plan(I, H, false, s_down, b_down);
+  if (packed && (!rgu.kw || !rgu2.kw || !rdn.kw))
+    return fail(DSPARK_ERR_UNSUPPORTED,
+                "moe_switch_glu_packed: H=%lld I=%lld need K %% 128 == 0 and 16-byte aligned scales and biases",
+                (long long)H, (long long)I);
+  if (packed) {
+    if ((st = launch_moe_rc<true, true>(rc_args(g), rgu, (int)E, bits, s))) return st;
+  } else if (rgu.kw && rgu2.kw) {
     if ((st = launch_moe_rc<true>(rc_args(g), rgu, (int)E, bits, s))) return st;
   } else if ((st = launch_moe_sk<true>(g, sb_checked(L.gu, {s_gate, b_gate, s_up, b_up}), (int)E, bits, s))) {
     return st;
@@ -694,8 +703,9 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   d.strips = L.dn.strips;
   d.mtiles = L.dn.mtiles;
   d.S = L.dn.S;
-  const RcPlan rdn = rc_plan(I, H, false, s_down, b_down);
-  if (rdn.kw) {
+  if (packed) {
+    if ((st = launch_moe_rc<false, true>(rc_args(d), rdn, (int)E, bits, s))) return st;
+  } else if (rdn.kw) {
     if ((st = launch_moe_rc<false>(rc_args(d), rdn, (int)E, bits, s))) return st;
   } else if ((st = launch_moe_sk<false>(d, sb_checked(L.dn, {s_down, b_down}), (int)E, bits, s))) {
     return st;
@@ -704,4 +714,31 @@ extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)M, (unsigned)((H + 255) / 256)), dim3(256), 0, s, ypair, pos,
                      scores_ws, static_cast<u16*>(out), (int)H, (int)k);
   return check_launch("moe combine");
+}
+}  // namespace
+}  // namespace dspark
+
+extern "C" int dspark_moe_switch_glu(const void* x, const void* logits, int64_t M, int64_t H, int64_t I, int64_t E,
+                                     int64_t k, int renorm, const uint32_t* w_gate, const void* s_gate,
+                                     const void* b_gate, const uint32_t* w_up, const void* s_up, const void* b_up,
+                                     const uint32_t* w_down, const void* s_down, const void* b_down, int bits,
+                                     int group_size, void* out, int32_t* inds, void* scores, void* workspace,
+                                     size_t workspace_bytes, dspark_stream stream) {
+  return switch_glu_impl(x, logits, M, H, I, E, k, renorm, w_gate, s_gate, b_gate, w_up, s_up, b_up, w_down, s_down,
+                         b_down, bits, group_size, out, inds, scores, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int dspark_moe_switch_glu_packed(const void* x, const void* logits, int64_t M, int64_t H, int64_t I,
+                                            int64_t E, int64_t k, int renorm, const void* w_gate,
+                                            const void* s_gate, const void* b_gate, const void* w_up,
+                                            const void* s_up, const void* b_up, const void* w_down,
+                                            const void* s_down, const void* b_down, int bits, int group_size,
+                                            void* out, int32_t* inds, void* scores, void* workspace,
+                                            size_t workspace_bytes, dspark_stream stream) {
+  if (H % 16 || I % 16)
+    return fail(DSPARK_ERR_SHAPE, "moe_switch_glu_packed: H=%lld and I=%lld must be multiples of 16", (long long)H,
+                (long long)I);
+  return switch_glu_impl(x, logits, M, H, I, E, k, renorm, static_cast<const uint32_t*>(w_gate), s_gate, b_gate,
+                         static_cast<const uint32_t*>(w_up), s_up, b_up, static_cast<const uint32_t*>(w_down), s_down,
+                         b_down, bits, group_size, out, inds, scores, workspace, workspace_bytes, stream, true);
 }

@@ -38,7 +38,10 @@ struct MoeRcArgs {
 
 // Requires K % 128 == 0, K <= KW * KSMAX * 64, N * K / 64 % 8 == 0 and 16-byte aligned scales
 // and biases. KSMAX (even) is the largest K part in groups.
-template <int BITS, int KSMAX, int KW, bool SWIGLU>
+// PW: the weights are dspark_moe_pack's form (each expert's 16-row tiles in the MFMA lane order,
+// one contiguous 1 KB wave read per group, or group pair at 4 bits), the same bytes per expert as
+// the row-major layout; scales and biases keep their layout. Same products, bit for bit.
+template <int BITS, int KSMAX, int KW, bool SWIGLU, bool PW = false>
 __global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_rc_kernel(const MoeRcArgs a) {
   constexpr int NT = 4 / KW;  // 16-column tiles per workgroup
   static_assert(KW == 1 || KW == 2 || KW == 4, "K parts");
@@ -97,7 +100,16 @@ __global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_r
   for (int i = 0; i < XCH; ++i) src[i] = src_row(0, xrow[i]);
   // ---- 2. weights of this wave's rows and K part
   WSlice<BITS, KSMAX> wsl;
-  wsl.load(wmat + (long)n * (K * BITS / 32), q, gs, gcount, G);
+  if constexpr (PW) {
+    constexpr int NL = BITS == 4 ? KSMAX / 2 : KSMAX;
+    const int per_tile = BITS == 4 ? (G >> 1) : G, first = BITS == 4 ? (gs >> 1) : gs;
+    const int nl = BITS == 4 ? (gcount >> 1) : gcount;
+    const char* tb = reinterpret_cast<const char*>(wmat) + (((long)(n >> 4) * per_tile + first) * 64 + lane) * 16;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) wsl.v[j] = ldg128_nt(tb + (long)min(j, nl - 1) * 1024);
+  } else {
+    wsl.load(wmat + (long)n * (K * BITS / 32), q, gs, gcount, G);
+  }
   // ---- 3. scale / bias blocks of the workgroup's tiles: 16 rows x G contiguous bf16 per
   // (array, tile), read in 16-byte chunks (2G per block; the last strip's block stops at the
   // matrix end)
@@ -119,7 +131,7 @@ __global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_r
 #pragma unroll
   for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (BITS == 4) swap_pairs(wsl);
+  if constexpr (BITS == 4 && !PW) swap_pairs(wsl);  // the packed form is stored swapped
 
   const u16* xl = &xs[min(c16, RC - 1) * XP + k_quarter<BITS>(q)];
   const int nrow = max(n - (ncol - c16), 0);  // this lane's row in its tile block (0 past N)

@@ -382,6 +382,32 @@ extern "C" int dspark_qmm_pack(const uint32_t* w, const void* scales, const void
   return check_launch("dspark_qmm_pack");
 }
 
+// ---- packed expert weights for the fused MoE block: the weight part of the packed form over the
+// E * N rows of [E, N, K*bits/32] (16-row tiles never straddle two experts: N % 16 == 0)
+extern "C" size_t dspark_moe_packed_bytes(int64_t E, int64_t N, int64_t K, int bits, int group_size) {
+  if (E < 1 || N % 16 || check_common(1, K, N, bits, group_size) || K % 128) return 0;
+  return (size_t)packed_layout(E * N, K, bits).wchunks * 16;
+}
+
+extern "C" int dspark_moe_pack(const uint32_t* w, int64_t E, int64_t N, int64_t K, int bits, int group_size,
+                               void* packed, size_t packed_bytes, dspark_stream stream) {
+  int st = check_common(1, K, N, bits, group_size);
+  if (st) return st;
+  if (E < 1 || N % 16 || K % 128)
+    return fail(DSPARK_ERR_SHAPE, "moe_pack: E=%lld N=%lld K=%lld (N %% 16 == 0, K %% 128 == 0)", (long long)E,
+                (long long)N, (long long)K);
+  if (!w || !packed) return fail(DSPARK_ERR_ARG, "moe_pack: null pointer");
+  if (!aligned(w, 16) || !aligned(packed, 16)) return fail(DSPARK_ERR_ALIGN, "moe_pack: buffers must be 16-byte aligned");
+  const PackedLayout L = packed_layout(E * N, K, bits);
+  if (packed_bytes < (size_t)L.wchunks * 16)
+    return fail(DSPARK_ERR_WORKSPACE, "moe_pack: packed buffer %zu < %zu bytes", packed_bytes, (size_t)L.wchunks * 16);
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((L.wchunks + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), reinterpret_cast<const unsigned char*>(w), nullptr, nullptr,
+                     nullptr, nullptr, nullptr, (long)(E * N), (int)K, bits, L.wchunks, 0L,
+                     static_cast<unsigned char*>(packed));
+  return check_launch("dspark_moe_pack");
+}
+
 // ---- fused gate / up / SwiGLU over the pair form: rows of the pair buffer = 32 ceil(N / 16)
 namespace {
 long swiglu_rows(int64_t N) { return 32 * ((N + 15) / 16); }

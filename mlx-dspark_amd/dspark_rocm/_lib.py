@@ -136,6 +136,12 @@ SIGNATURES: dict[str, tuple] = {
                                       c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_size_t, c_void_p]),
     "dspark_moe_workspace": (c_size_t, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "dspark_moe_packed_bytes": (c_size_t, [c_i64, c_i64, c_i64, c_int, c_int]),
+    "dspark_moe_pack": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "dspark_moe_switch_glu_packed": (c_int, [c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64, c_int,
+                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_size_t, c_void_p]),
     "dspark_rmsnorm": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_float, c_void_p, c_i64,
                                c_void_p, c_i64, c_void_p]),
     "dspark_qk_norm_rope_kv": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64,

@@ -111,6 +111,13 @@ class SwitchGLU(nn.Module):
                    QuantizedSwitchLinear.random(experts, intermediate, hidden, bits=bits, device=device, generator=generator),
                    QuantizedSwitchLinear.random(experts, hidden, intermediate, bits=bits, device=device, generator=generator))
 
+    def pack(self) -> "SwitchGLU":
+        """Pack the three projections' expert weights for the fused block (bit-identical
+        products; the row-major weights stay for the unfused path)."""
+        for lin in (self.gate_proj, self.up_proj, self.down_proj):
+            lin.pack()
+        return self
+
     def _proj(self, lin: QuantizedSwitchLinear, x, idx, sorted_indices):
         return gather_qmm(x, *lin.triple(), rhs_indices=idx, bits=lin.bits, group_size=lin.group_size,
                           sorted_indices=sorted_indices)
@@ -149,8 +156,8 @@ class SparseMoeBlock(nn.Module):
         x2 = x.reshape(-1, x.shape[-1])
         logits = self.router_logits(x2)
         mlp = self.switch_mlp
-        out, _, _ = ops.moe_switch_glu(x2, logits, mlp.gate_proj.triple(), mlp.up_proj.triple(),
-                                       mlp.down_proj.triple(), k=self.top_k, bits=mlp.gate_proj.bits,
+        out, _, _ = ops.moe_switch_glu(x2, logits, mlp.gate_proj.fused_triple(), mlp.up_proj.fused_triple(),
+                                       mlp.down_proj.fused_triple(), k=self.top_k, bits=mlp.gate_proj.bits,
                                        renorm=self.norm_topk_prob, group_size=mlp.gate_proj.group_size)
         return out.reshape(*lead, out.shape[-1])
 

@@ -118,3 +118,15 @@ class QuantizedSwitchLinear(nn.Module):
 
     def triple(self):
         return self.weight, self.scales, self.biases
+
+    def pack(self) -> None:
+        """Hold the weights (also) in the packed expert form (``ops.moe_pack``), which the fused
+        MoE block then reads; products are bit-identical."""
+        from . import ops
+
+        self.packed = ops.moe_pack(self.weight, bits=self.bits, group_size=self.group_size)
+
+    def fused_triple(self):
+        """(weights, scales, biases) for the fused block: the packed form when held."""
+        packed = getattr(self, "packed", None)
+        return (packed if packed is not None else self.weight), self.scales, self.biases

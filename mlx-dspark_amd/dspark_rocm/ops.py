@@ -543,11 +543,40 @@ def gather_qmm_sorted(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bi
     return y
 
 
+class PackedExperts:
+    """Stacked expert weights [E, N, K*bits/32] in the packed form of ``dspark_moe_pack``: each
+    expert's 16-row tiles in the MFMA lane order (the same bytes; scales and biases are not part
+    of it and keep their [E, N, K/64] layout)."""
+
+    def __init__(self, buf: torch.Tensor, experts: int, n: int, k: int, bits: int):
+        self.buf, self.experts, self.n, self.k, self.bits = buf, experts, n, k, bits
+
+
+def moe_packable(experts: int, n: int, k: int, bits: int, group_size: int = GROUP) -> bool:
+    return int(_lib.load().dspark_moe_packed_bytes(experts, n, k, bits, group_size)) > 0
+
+
+def moe_pack(w: torch.Tensor, *, bits: int, group_size: int = GROUP) -> PackedExperts:
+    """Pack stacked expert weights (int32 [E, N, K*bits/32]) once (N % 16 == 0, K % 128 == 0)."""
+    _require_cuda(w)
+    _require_packed(w)
+    E, n, k = w.shape[0], w.shape[1], w.shape[2] * 32 // bits
+    w = w.contiguous()
+    nbytes = int(_lib.load().dspark_moe_packed_bytes(E, n, k, bits, group_size))
+    if nbytes == 0:
+        raise _lib.DsparkError("dspark_moe_pack", -2, f"[{E}, {n}, {k}] {bits}-bit cannot be packed "
+                                                      "(N % 16 == 0 and K % 128 == 0 needed)")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _lib.call("dspark_moe_pack", _ptr(w), E, n, k, bits, group_size, _ptr(buf), nbytes, _stream(w))
+    return PackedExperts(buf, E, n, k, bits)
+
+
 def moe_switch_glu(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: int, bits: int = 4,
                    renorm: bool = True, group_size: int = GROUP):
     """Routed-expert SwiGLU MLP of one MoE block: route -> gate/up (fused SwiGLU) -> down ->
     score-weighted combine, four launches. ``gate``/``up``/``down`` are (w, scales, biases) with
-    w packed [E, rows, cols*bits/32]. Returns (out bf16 [M, H], inds [M, k], scores [M, k])."""
+    w int32 [E, rows, cols*bits/32], or a :class:`PackedExperts` of it (``dspark_moe_switch_glu_packed``,
+    the same results bit for bit). Returns (out bf16 [M, H], inds [M, k], scores [M, k])."""
     _require_cuda(x, logits)
     _require_bf16("x", x)
     _require_bf16("logits", logits)
@@ -555,7 +584,10 @@ def moe_switch_glu(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: 
     logits = logits.contiguous()
     M, H = x.shape
     E = logits.shape[1]
-    I = gate[0].shape[1]
+    packed = isinstance(gate[0], PackedExperts)
+    if packed != isinstance(up[0], PackedExperts) or packed != isinstance(down[0], PackedExperts):
+        raise ValueError("moe_switch_glu: gate, up and down must all be packed or all row-major")
+    I = gate[0].n if packed else gate[0].shape[1]
     lib = _lib.load()
     nbytes = lib.dspark_moe_workspace(M, H, I, E, k)
     if nbytes == 0:
@@ -565,9 +597,12 @@ def moe_switch_glu(x: torch.Tensor, logits: torch.Tensor, gate, up, down, *, k: 
     inds = torch.empty((M, k), dtype=torch.int32, device=x.device)
     scores = torch.empty((M, k), dtype=torch.bfloat16, device=x.device)
     (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
-    _lib.call("dspark_moe_switch_glu", _ptr(x), _ptr(logits), M, H, I, E, k, int(bool(renorm)),
-              _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu), _ptr(su), _ptr(bu), _ptr(wd), _ptr(sd), _ptr(bd),
-              bits, group_size, _ptr(out), _ptr(inds), _ptr(scores), _ptr(ws), ws.numel(), _stream(x))
+    if packed:
+        wg, wu, wd = wg.buf, wu.buf, wd.buf
+    _lib.call("dspark_moe_switch_glu_packed" if packed else "dspark_moe_switch_glu", _ptr(x), _ptr(logits), M, H, I,
+              E, k, int(bool(renorm)), _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu), _ptr(su), _ptr(bu), _ptr(wd),
+              _ptr(sd), _ptr(bd), bits, group_size, _ptr(out), _ptr(inds), _ptr(scores), _ptr(ws), ws.numel(),
+              _stream(x))
     return out, inds, scores
 
 

@@ -107,3 +107,46 @@ def test_switch_glu(dev, M, E, k, H, I, bits):
     import torch
 
     assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("M,E,k,H,I,bits", [(16, 8, 2, 256, 128, 4), (16, 128, 8, 2048, 768, 4),
+                                             (16, 128, 8, 2048, 768, 8), (16, 2, 2, 512, 256, 4),
+                                             (33, 4, 2, 256, 4096, 8)])
+def test_switch_glu_packed_experts_bitwise(dev, M, E, k, H, I, bits):
+    """The packed expert form (dspark_moe_pack) gives the row-major block's output bit for bit
+    (same K parts, same per-group arithmetic and order), and its bytes are the weight part of the
+    dense packed layout of each expert's matrix."""
+    import torch
+
+    from dspark_rocm import ops
+    from test_gpu_qmm_packed import _pack_np
+
+    r = rng(M + E + H + 1)
+    x = to_dev_bf16(randn_bf16(r, M, H), dev)
+    logits = to_dev_bf16(randn_bf16(r, M, E), dev)
+    g, u, d = _moe_weights(r, E, H, I, bits)
+    rm = [_dev3(t, dev) for t in (g, u, d)]
+    pk = [(ops.moe_pack(w, bits=bits), s, b) for (w, s, b) in rm]
+    out, inds, scores = ops.moe_switch_glu(x, logits, *rm, k=k, bits=bits)
+    out_p, inds_p, scores_p = ops.moe_switch_glu(x, logits, *pk, k=k, bits=bits)
+    assert torch.equal(inds_p, inds) and torch.equal(scores_p, scores)
+    assert torch.equal(out_p, out)
+    # layout: expert e's bytes are the weight tiles of its [n, kk] matrix in the dense packed form
+    w, s, b = d
+    n, kk = w.shape[1], w.shape[2] * 32 // bits
+    got = pk[2][0].buf.cpu().numpy().reshape(E, -1)
+    wbytes = got.shape[1]
+    for e in (0, E - 1):
+        assert np.array_equal(got[e], _pack_np(w[e], s[e], b[e], n, kk, bits)[:wbytes])
+
+
+def test_moe_pack_refusals(dev):
+    import torch
+
+    from dspark_rocm import _lib, ops
+
+    assert ops.moe_packable(4, 768, 2048, 4) and not ops.moe_packable(4, 760, 2048, 4)   # N % 16
+    assert not ops.moe_packable(4, 2048, 192, 8)                                          # K % 128
+    w = torch.zeros((4, 2048, 192 // 4), dtype=torch.int32, device=dev)
+    with pytest.raises(_lib.DsparkError):
+        ops.moe_pack(w, bits=8)
