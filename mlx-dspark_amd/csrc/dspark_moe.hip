@@ -412,6 +412,7 @@ MoePlan moe_plan(long K, long N, long E, long M, bool swiglu, int bits) {
   long s = (G + 15) / 16;
   if (E * p.strips * p.mtiles * s < 512) s = (G + 7) / 8;
   if (s > kQmmMaxSlices) s = kQmmMaxSlices;
+  if (s > max_slices(G, bits)) s = max_slices(G, bits);
   if (s < 1) s = 1;
   p.S = (int)s;
   p.ksmax = slice_capacity(G, s, bits);

@@ -73,6 +73,7 @@ Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
     if (w16 <= 2 * slots16 && fill(w16, slots16) < 0.9 && fill(strips * s8, slots8) > fill(w16, slots16)) s = s8;
   }
   if (s > kQmmMaxSlices) s = kQmmMaxSlices;
+  if (s > max_slices(G, bits)) s = max_slices(G, bits);
   if (s < 1) s = 1;
   p.S = (int)s;
   p.ksmax = slice_capacity(G, s, bits);

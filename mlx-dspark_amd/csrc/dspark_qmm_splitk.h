@@ -76,10 +76,18 @@ __host__ __device__ inline void slice_groups(int sl, int S, int G, int unit, int
   ge = min(unit * (((sl + 1) * units) / S), G);
 }
 
+// Most slices G groups can be cut into with none of them empty.
+inline long max_slices(long G, int bits) {
+  const long unit = slice_unit((int)G, bits);
+  return (G + unit - 1) / unit;
+}
+
 // Kernel instantiation (8 or 16 groups) that holds the largest of S slices of G groups, or 0
-// when a slice would exceed 16 groups (K > 32768 at 32 slices).
+// when a slice would exceed 16 groups (K > 32768 at 32 slices) or S would leave a slice empty
+// (the kernels read group gs - 1 of an empty slice).
 inline int slice_capacity(long G, long S, int bits) {
   const long unit = slice_unit((int)G, bits), units = (G + unit - 1) / unit;
+  if (S < 1 || S > units) return 0;
   const long per = unit * ((units + S - 1) / S);
   return per <= 8 ? 8 : per <= 16 ? 16 : 0;
 }

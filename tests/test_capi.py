@@ -58,6 +58,36 @@ def test_plan_blocks_scale_with_length():
     assert lib.dspark_verify_attention_workspace(1, 32, 8, 16, 128, 64) == 0   # one block: no partials
 
 
+def test_split_k_plans_never_leave_a_slice_empty():
+    """Every plan the library picks cuts K into S non-empty slices that fit the kernel
+    instantiation (an empty slice would make the kernel read the group before its first one).
+    The cut (multiples of 8 groups when G % 8 == 0, else of 2 for 4-bit rows, else 1, slice
+    sl starting at unit * floor(sl * units / S)) is checked as a partition of [0, G)."""
+    import ctypes
+
+    from dspark_rocm import _lib
+
+    lib = _lib.load()
+    out = (ctypes.c_int32 * 4)()
+    checked = 0
+    for bits in (4, 8):
+        for g in list(range(1, 80)) + [96, 128, 160, 192, 256, 320, 384, 400, 512]:
+            K = 64 * g
+            for N in (16, 64, 1024, 4096, 6144, 151936):
+                for M in (1, 16, 64):
+                    if lib.dspark_qmm_affine_plan(M, K, N, bits, 64, out) != 0:
+                        continue
+                    S, ksmax = out[0], out[1]
+                    unit = 8 if g % 8 == 0 else 2 if bits == 4 else 1
+                    units = -(-g // unit)
+                    cuts = [min(unit * ((sl * units) // S), g) for sl in range(S + 1)]
+                    sizes = [b - a for a, b in zip(cuts, cuts[1:])]
+                    assert cuts[0] == 0 and cuts[-1] == g, (bits, K, N, M, S)
+                    assert min(sizes) >= 1 and max(sizes) <= ksmax, (bits, K, N, M, S, sizes)
+                    checked += 1
+    assert checked > 1000
+
+
 def test_noalloc_qmm_refuses_oversize_before_any_gpu_call():
     """A shape whose split-K scratch exceeds the library-held array is refused on the host
     (DSPARK_ERR_WORKSPACE) before any HIP call: the pointers below are never dereferenced."""
