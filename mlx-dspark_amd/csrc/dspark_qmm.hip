@@ -30,6 +30,7 @@
 #include <mutex>
 
 #include "dspark_qmm_splitk.h"
+#include "dspark_qmm_wholek.h"
 
 namespace dspark {
 namespace {
@@ -46,6 +47,8 @@ constexpr size_t kMaxCounters = kCtrRegionBytes / sizeof(int);
 // Launch plan shared by the workspace query and the launch: S depends only on the strips and
 // K, never on M, so a row's result does not depend on how many rows ride with it.
 struct Plan {
+  bool wholek;  // 16-row whole-K workgroups (qmm_wk_kernel), no split-K and no workspace
+  int tiles;    // wholek: 16-row output tiles over all problems
   int S;       // K slices
   int ksmax;   // groups per slice the kernel is instantiated for (8, 16 or 32)
   int strips;  // 64-row strips over all problems
@@ -54,13 +57,29 @@ struct Plan {
   size_t part_bytes;
 };
 
-Plan make_plan(const long* Ns, int count, long K, long M, int bits) {
+// wholek_ok: the launch may take the whole-K kernel (the plain qmm entry points, not the fused
+// SwiGLU pair, whose epilogue only the split-K kernel has).
+Plan make_plan(const long* Ns, int count, long K, long M, int bits, bool wholek_ok = false) {
   Plan p{};
   const long G = K / 64;
   long strips = 0;
   for (int i = 0; i < count; ++i) strips += (Ns[i] + kStripRows - 1) / kStripRows;
   p.strips = (int)strips;
   p.mtiles = (int)((M + 15) / 16);
+  // One 16-row whole-K workgroup per CU where it was measured faster than split-K: 8-bit rows,
+  // K = 4096, 240..256 tiles (a [4096, 4096] matrix, or problems adding up to it). The choice
+  // depends on the shape only, never on M, so a row's bits do not depend on its company.
+  if (wholek_ok && bits == 8 && K == 4096) {
+    long tiles = 0;
+    for (int i = 0; i < count; ++i) tiles += (Ns[i] + 15) / 16;
+    if (tiles >= 240 && tiles <= kCUs) {
+      p.wholek = true;
+      p.tiles = (int)tiles;
+      p.S = 1;
+      p.ksmax = (int)G;
+      return p;
+    }
+  }
   // 16 groups (1024 k) per slice, unless those workgroups fill their last resident round
   // (one or two rounds) poorly and 8-group slices, whose kernels keep more workgroups per CU,
   // fill theirs better. Resident workgroups per CU of the instantiations (VGPR-limited, as
@@ -104,6 +123,15 @@ template <int BITS>
 int launch_bits(const QmmSkArgs& a, const Plan& p, bool sbvec, hipStream_t st) {
   if (p.ksmax == 8) return sbvec ? launch<BITS, 8, true>(a, p, st) : launch<BITS, 8, false>(a, p, st);
   return sbvec ? launch<BITS, 16, true>(a, p, st) : launch<BITS, 16, false>(a, p, st);
+}
+
+constexpr int kWkWaves = 8;  // whole-K: one K octet per wave at K = 4096
+
+template <bool PACKED, bool SBVEC>
+int launch_wk(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
+  hipLaunchKernelGGL((qmm_wk_kernel<8, kWkWaves, PACKED, SBVEC>), dim3(p.tiles, p.mtiles), dim3(64 * kWkWaves), 0, st,
+                     a);
+  return check_launch(PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
 }
 
 template <int BITS, bool SWIGLU = false>
@@ -228,7 +256,7 @@ extern "C" int dspark_qmm_affine_supported(int64_t M, int64_t K, int64_t N, int 
   const int st = check_common(M, K, N, bits, group_size);
   if (st) return st;
   long Ns[1] = {(long)N};
-  if (make_plan(Ns, 1, K, M, bits).S == 0)
+  if (make_plan(Ns, 1, K, M, bits, true).S == 0)
     return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld x N=%lld x K=%lld needs more than %zu split-K counters or 32 slices",
                 (long long)M, (long long)N, (long long)K, kMaxCounters);
   return DSPARK_OK;
@@ -239,11 +267,11 @@ extern "C" int dspark_qmm_affine_plan(int64_t M, int64_t K, int64_t N, int bits,
   const int st = dspark_qmm_affine_supported(M, K, N, bits, group_size);
   if (st) return st;
   long Ns[1] = {(long)N};
-  const Plan p = make_plan(Ns, 1, K, M, bits);
+  const Plan p = make_plan(Ns, 1, K, M, bits, true);
   out[0] = p.S;
   out[1] = p.ksmax;
   out[2] = p.strips;
-  out[3] = p.S * p.strips * p.mtiles;
+  out[3] = p.wholek ? p.tiles * p.mtiles : p.S * p.strips * p.mtiles;
   return DSPARK_OK;
 }
 
@@ -251,14 +279,14 @@ extern "C" size_t dspark_qmm_affine_multi_workspace(const dspark_qmm_problem* pr
                                                     int bits, int group_size) {
   long Ns[kQmmMaxProblems];
   if (validate(problems, count, M, bits, group_size, Ns)) return 0;
-  const Plan p = make_plan(Ns, count, problems[0].K, M, bits);
+  const Plan p = make_plan(Ns, count, problems[0].K, M, bits, true);
   return p.ctr_bytes + p.part_bytes;
 }
 
 extern "C" size_t dspark_qmm_affine_workspace(int64_t M, int64_t K, int64_t N, int bits, int group_size) {
   if (check_common(M, K, N, bits, group_size)) return 0;
   long Ns[1] = {(long)N};
-  const Plan p = make_plan(Ns, 1, K, M, bits);
+  const Plan p = make_plan(Ns, 1, K, M, bits, true);
   return p.ctr_bytes + p.part_bytes;
 }
 
@@ -272,7 +300,7 @@ int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bit
   int st = validate(problems, count, M, bits, group_size, Ns, packed);
   if (st) return st;
   const long K = problems[0].K;
-  const Plan p = make_plan(Ns, count, K, M, bits);
+  const Plan p = make_plan(Ns, count, K, M, bits, true);
   if (p.S == 0)
     return fail(DSPARK_ERR_SHAPE, "qmm: M=%lld K=%lld needs more than %zu split-K counters or 32 slices", (long long)M,
                 (long long)K, kMaxCounters);
@@ -315,6 +343,15 @@ int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bit
   for (int i = count; i < kQmmMaxProblems; ++i) {
     a.p[i] = a.p[0];
     a.p[i].strip0 = 1 << 30;
+  }
+  if (p.wholek) {  // blockIdx.x counts 16-row tiles
+    int t0 = 0;
+    for (int i = 0; i < count; ++i) {
+      a.p[i].strip0 = t0;
+      t0 += (int)((problems[i].N + 15) / 16);
+    }
+    if (packed) return launch_wk<true, true>(a, p, s);
+    return sbvec ? launch_wk<false, true>(a, p, s) : launch_wk<false, false>(a, p, s);
   }
   if (packed) return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
   return bits == 4 ? launch_bits<4>(a, p, sbvec, s) : launch_bits<8>(a, p, sbvec, s);
@@ -704,7 +741,7 @@ extern "C" int dspark_qmm_affine_noalloc(const void* x, int64_t ldx, int64_t M, 
   long Ns[1];
   int st = validate(&p, 1, M, bits, group_size, Ns);
   if (st) return st;
-  const Plan pl = make_plan(Ns, 1, K, M, bits);
+  const Plan pl = make_plan(Ns, 1, K, M, bits, true);
   if (pl.S == 0)
     return fail(DSPARK_ERR_SHAPE, "qmm_affine_noalloc: M=%lld x N=%lld x K=%lld is not supported", (long long)M,
                 (long long)N, (long long)K);

@@ -228,14 +228,21 @@ def test_skinny_plan_geometry():
     for n, k in ((4096, 4096), (24576, 4096), (4096, 12288), (1024, 4096), (64, 4096), (1024, 1024)):
         p = sk.plan(16, n, k, 8)
         assert p["strips"] == -(-n // 64)
-        assert p["workgroups"] == p["slices"] * p["strips"]
+        if (n, k) == (4096, 4096):
+            # 8-bit [4096, 4096]: one 16-row workgroup per tile over all of K, no workspace
+            assert (p["slices"], p["groups_per_slice"], p["workgroups"]) == (1, 64, 256)
+        else:
+            assert p["workgroups"] == p["slices"] * p["strips"]
+            assert p["groups_per_slice"] in (8, 16, 32)
         assert p["slices"] * p["groups_per_slice"] >= k // 64
-        assert p["groups_per_slice"] in (8, 16, 32)
         assert (p["workspace_bytes"] > 0) == (p["slices"] > 1)
         assert p | {"rows": 5} == sk.plan(5, n, k, 8)   # the plan does not depend on M (<= 16)
-    # the same K split serves 4 and 8 bits
-    assert sk.plan(16, 4096, 4096, 4)["slices"] == sk.plan(16, 4096, 4096, 8)["slices"]
-    assert sk.geometry(4096, 4096) == (64, 8)
+        assert sk.plan(33, n, k, 8)["slices"] == p["slices"]   # nor does the kernel choice, at any M
+    # the same K split serves 4 and 8 bits (the whole-K launch is 8-bit only)
+    assert sk.plan(16, 4096, 12288, 4)["slices"] == sk.plan(16, 4096, 12288, 8)["slices"]
+    assert sk.plan(16, 4096, 4096, 4)["slices"] == 8
+    assert sk.geometry(4096, 4096) == (64, 1)
+    assert sk.geometry(4096, 4096, bits=4) == (64, 8)
 
 
 def _qlinear(bits=4, out_features=64, in_features=128, bias=False):
