@@ -9,9 +9,11 @@
 // A operand) are read straight from global memory (x is small and stays in L2), the weight
 // fragment from the row (or the packed tile stream), and the bias term's per-row sum of x comes
 // from the same MFMA against an all-ones B operand, in the output layout. Same per-group
-// arithmetic as qmm_sk_kernel (acc = fma(b, sum x, fma(s, P, acc)) with P exact in fp32); the
-// sums of x and the association of the wave partials differ, so the bits are this kernel's own
-// (equal between the row-major and packed weight layouts, and for every M).
+// arithmetic as qmm_sk_kernel (acc = fma(b, sum x, fma(s, P, acc)) with P exact in fp32). With
+// one octet per wave (NW = G / 8) the octet partials and their wave-order sum are the split-K
+// plan's 8-group slices summed in slice order, so the two kernels agree bit for bit wherever the
+// per-group sums of x (here an MFMA against ones, there lane sums) are exact in fp32, as they are
+// for bf16 x of ordinary range. Row-major and packed weights give the same bits, at every M.
 #pragma once
 
 #include "dspark_qmm_splitk.h"
