@@ -437,6 +437,9 @@ def bench_prefill_wide(dev, n: int = 12288, k: int = 4096, bits: int = 8, widths
     return out
 
 
+DSPARK_TAP = (5, 17, 29, 41, 46)
+
+
 def bench_verify_forward(dev, context: int = 16384, rows: int = 16, widths=(1, 2, 4, 8, 16), shallow: int = 512):
     """Speculative verify steps of a random-init dense 8-bit 64-layer target (hidden 5120, heads
     64/8 x 128, intermediate 25600, vocab 151936, RoPE 1e6) over a synthetic bf16 KV cache:
@@ -470,6 +473,10 @@ def bench_verify_forward(dev, context: int = 16384, rows: int = 16, widths=(1, 2
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     e = tgt.engine
+    # the drafter's hidden-state tap, as a DSpark round verifies with it (generate.py:1547): the
+    # reference's default target_layer_ids (config.py:233); the tapped residual streams are
+    # written where the step forms them, no extra launch
+    e.set_tap(DSPARK_TAP)
     # self-consistent drafts: the step's own target tokens fed back until they stop changing
     seq = torch.randint(0, args.vocab_size, (rows,), generator=g, device=dev).tolist()
     passes = 0
@@ -507,7 +514,7 @@ def bench_verify_forward(dev, context: int = 16384, rows: int = 16, widths=(1, 2
     res = {"layers": 64, "hidden": 5120, "context": context, "rows": rows, "weight_bytes": weights, "kv_bytes": kv,
            "bytes": by, "ms_graph": round(ms, 4), "GBs": round(by / (ms * 1e-3) / 1e9, 1),
            "frac_of_peak": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "accepted": accepted,
-           "accepted_expected": rows - 1, "draft_passes": passes, "launches": 64 * 9 + 4,
+           "accepted_expected": rows - 1, "draft_passes": passes, "launches": 64 * 9 + 4, "tap": list(e.tap),
            "build_s": round(build_s, 1),
            "curve": curve, "depth_slope_us_per_token": slope}
     del model, tgt, cache, e

@@ -123,6 +123,18 @@ int dspark_qmm_affine_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
                               int64_t N, int bits, int group_size,
                               void* y, int64_t ldy, dspark_stream stream);
 
+/* Clear the split-K arrival counters of dspark_qmm_affine_noalloc's array on the current GPU
+ * (a fill kernel on `stream`, no allocation). Every completed call leaves them at zero; a call
+ * that did not complete (a launch error or an aborted stream) can leave them stale, and every
+ * later call on that GPU would then mis-sum. No counterpart in the reference: for the same
+ * callers that cannot allocate, as the recovery step after such a failure. */
+int dspark_qmm_noalloc_reset(dspark_stream stream);
+
+/* Device address and size of dspark_qmm_affine_noalloc's array on the current GPU (looked up
+ * and its counters cleared on first use, as the entry point does). No counterpart in the
+ * reference: diagnostics and tests of the no-allocation entry point. */
+int dspark_qmm_noalloc_scratch(void** ptr, size_t* bytes);
+
 /*
  * Dequantize once, for the prefill wide path: out[n, j] = (scale[n, j/64] * q[n, j]) + bias[n, j/64]
  * for the reference-layout matrix of dspark_qmm_affine, each operation an fp32 operation rounded
@@ -147,7 +159,13 @@ int dspark_stream_read(const void* p, size_t bytes, uint32_t* sink, dspark_strea
 /* One launch over up to DSPARK_QMM_MAX_PROBLEMS matrices that share bits, group size, M and K
  * (q/k/v of an attention block, gate/up of an MLP). Each problem has its own x, w, scales,
  * biases and y. Replaces the per-projection QuantizedLinear calls of one decoder layer
- * (target.py:208-221 -> mlx-lm DecoderLayer), which the reference launches one by one. */
+ * (target.py:208-221 -> mlx-lm DecoderLayer), which the reference launches one by one.
+ * Results equal separate dspark_qmm_affine calls bit for bit, with one qualification: an 8-bit
+ * [4096, 4096] matrix alone takes the whole-K kernel, whose per-group sums of x come from an MFMA
+ * against ones, while in a launch with other matrices it takes split-K, whose sums are lane
+ * sums. The two agree whenever those fp32 sums are exact (bf16 x of ordinary range); with x
+ * spanning many binades in one group of 64 they can differ by an fp32 rounding of the bias
+ * term, well inside the qmm tolerance. */
 #define DSPARK_QMM_MAX_PROBLEMS 4
 typedef struct dspark_qmm_problem {
   const void* x;
@@ -244,7 +262,9 @@ size_t dspark_qmm_swiglu_packed_workspace(int64_t N, int64_t K, int64_t M, int b
  * out      bf16 [B, Hq, Mq, D] contiguous
  * workspace  device buffer of at least dspark_verify_attention_workspace(...) bytes
  *            (fp32 split-KV partials); may be NULL when that size is 0.
- * D in {64, 128, 256}; Hq % Hk == 0; gqa * Mq <= 256.
+ * D % 8 == 0, 8 <= D <= 256 (the reference's rule, multirow_attn.py:200; kernel instances at
+ * 64, 128 and 256 columns, a smaller head dim's missing columns zero on chip and never read or
+ * written in memory); Hq % Hk == 0; gqa * Mq <= 256.
  *
  * Replaces multirow_attn.multirow_sdpa(q, k, v, scale=, causal=, tree_anc=)
  * (multirow_attn.py:223-259): the dspark_mra_p1 / _p1_tree / _p2 Metal kernels
@@ -295,9 +315,11 @@ int dspark_verify_attention_typed(int dtype, const void* q, int64_t B, int64_t H
  *           (strides k_scale_strides / v_scale_strides in elements, shared by scales and biases).
  * Each value is scale * field + bias (group_size 64). The reference's own multirow kernel does
  * not read this format (quantized caches fall through to mlx-lm's quantized SDPA,
- * multirow_attn.py:288-299); this entry point serves that fall-through on the same kernel: the
- * tile loader dequantizes to the compute type (fp32 fma, one rounding) and the MFMA loop, mask,
- * softmax and split-KV combine are those of dspark_verify_attention_typed. No tree mask.
+ * multirow_attn.py:288-299); this entry point serves that fall-through on the same kernel in the
+ * factored form of the quantized matmul: the integer fields go through the MFMA exactly, and the
+ * per-(key, group) scales and biases are applied in fp32 (scores: scale_k * (f . q) + bias_k *
+ * sum q; output: (p * scale_v) . f_v + sum p * bias_v). Mask, softmax and split-KV combine are
+ * those of dspark_verify_attention_typed. D in {64, 128, 256}. No tree mask.
  */
 int dspark_verify_attention_quantized(int dtype, const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
                                       const uint32_t* k_words, const void* k_scales, const void* k_biases,
@@ -418,7 +440,7 @@ int dspark_rmsnorm(const void* x, int64_t ldx, const void* r, int64_t ldr, const
  *   q_out [Hq, M, D] (contiguous; the attention q input, batch 1),
  *   k_cache[h * k_cache_strides[0] + (pos0 + m) * k_cache_strides[1] + d] = rotated k,
  *   v_cache[...same with v strides...] = v.
- * q [M, ldq >= Hq*D], k/v [M, ld >= Hk*D] are the q/k/v projections; D in {64, 128}.
+ * q [M, ldq >= Hq*D], k/v [M, ld >= Hk*D] are the q/k/v projections; D % 8 == 0, D <= 256.
  * Replaces Attention.__call__'s q_norm/k_norm, rope(offset=cache.offset) and
  * cache.update_and_fetch (mlx-lm qwen3; the cache write of batch_engine.py:193-219). */
 int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,

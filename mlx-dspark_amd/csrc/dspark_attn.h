@@ -103,6 +103,7 @@ struct AttnArgs {
   long qvsb, qvsh, qvss;
   long osb, osh, osi;     // output strides (batch, query head, position); head_dim contiguous
   int Hq, Hk, Mq, L;
+  int dv;                 // the caller's head dim (a multiple of 8, <= the instance's D)
   int gqa, R, RT, RP;
   int chunk, NB;
   float scale_log2;
@@ -201,20 +202,26 @@ __device__ __forceinline__ void fields8(const u32* w, int first, u32* out) {
   }
 }
 
-// 4-bit fields of word w as 8 T values off + f, in the order (f0, f4, f1, f5, f2, f6, f3, f7):
-// one v_and_or_b32 per pair (off = 128 for bf16, 0x43004300 being the pair (128, 128); 1024
-// for fp16, 0x64006400); the matching x / q order is perm_x_u4's
+// 4-bit fields of word w as 8 T values, in the order (f0, f4, f1, f5, f2, f6, f3, f7), the
+// matching x / q order being perm_x_u4's. One v_and_or_b32 per pair makes (off + f_t,
+// off + f_{t+4}): bf16 off = 128 (0x43004300 is the pair (128, 128)), which the tables take
+// back out (bias - 128 * scale); fp16 off = 1024 (0x6400), which one packed fp16 subtract per
+// pair removes exactly here, so fp16 values are the fields themselves (no large offset term
+// cancels in an fp32 sum: with 1024 in the tables, their rounding grew about 1024-fold)
 template <class T>
 __device__ __forceinline__ u32x4_t unpack4_off(u32 w) {
   if constexpr (T::kF16) {
     const u32 m = 0x000F000Fu, c = 0x64006400u;
-    return u32x4_t{and_or(w, m, c), and_or(w >> 4, m, c), and_or(w >> 8, m, c), and_or(w >> 12, m, c)};
+    const f16x2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    auto pair = [&](u32 x) { return __builtin_bit_cast(u32, __builtin_bit_cast(f16x2_t, and_or(x, m, c)) - off); };
+    return u32x4_t{pair(w), pair(w >> 4), pair(w >> 8), pair(w >> 12)};
   } else {
     return unpack_u4(w);
   }
 }
+// offset left in the staged 4-bit fields (removed through the bias tables)
 template <class T>
-constexpr float kOff4 = T::kF16 ? 1024.0f : 128.0f;
+constexpr float kOff4 = T::kF16 ? 0.0f : 128.0f;
 
 // ---------------------------------------------------------------- pass 1
 
@@ -276,10 +283,12 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   // ---- this lane's query row (B operand of S^T = K Q^T), over the whole head dim
   const int rr = min(rt * 16 + c16, a.R - 1);
   const int qi = rr % a.Mq;
-  const u16* qrow = a.q + ((long)(b * a.Hq + hk * a.gqa) * a.Mq + rr) * D;
+  const u16* qrow = a.q + ((long)(b * a.Hq + hk * a.gqa) * a.Mq + rr) * a.dv;
   u32x4_t qf[NDC];
+  // head dims below the instance's D: the missing columns of q, K and V are zeros (never read)
 #pragma unroll
-  for (int c = 0; c < NDC; ++c) qf[c] = ldg128(qrow + 32 * c + 8 * q4);
+  for (int c = 0; c < NDC; ++c)
+    qf[c] = 32 * c + 8 * q4 < a.dv ? ldg128(qrow + 32 * c + 8 * q4) : u32x4_t{0u, 0u, 0u, 0u};
   if constexpr (QB == 4) {
     // 4-bit K fields sit in LDS in unpack4_off's order: q follows (its row sums do not change)
 #pragma unroll
@@ -317,6 +326,10 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   //    and biases of K and V into the tile's fp32 tables.
   const bool vthread = tid < VQ * DC;
   const int vkq = tid % VQ, vdc = tid / VQ;
+  // a thread's K chunks all sit in column tid % DC (THREADS is a multiple of DC), its V chunks in
+  // column vdc: columns at or past the head dim load nothing and stage zeros
+  const bool kcol = 8 * (tid % DC) < a.dv, vcol = 8 * vdc < a.dv;
+  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
   const u16* kbase16 = static_cast<const u16*>(a.k) + b * a.ksb + hk * a.ksh;
   const u16* vbase16 = static_cast<const u16*>(a.v) + b * a.vsb + hk * a.vsh;
   const u32* kbase32 = static_cast<const u32*>(a.k) + b * a.ksb + hk * a.ksh;
@@ -338,10 +351,10 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
       const char* vb = reinterpret_cast<const char*>(vbase16 + (long)kt * a.vss);
 #pragma unroll
       for (int j = 0; j < LOADS; ++j)
-        if (!KPART || tid + THREADS * j < KT * DC) r.k[j] = ldg128((kb + j * kstep) + koff);
+        if (!KPART || tid + THREADS * j < KT * DC) r.k[j] = kcol ? ldg128((kb + j * kstep) + koff) : zero4;
       if (vthread) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r.v[j] = ldg128((vb + (long)j * a.vss * 2) + voff);
+        for (int j = 0; j < 4; ++j) r.v[j] = vcol ? ldg128((vb + (long)j * a.vss * 2) + voff) : zero4;
       }
       return;
     }
@@ -349,13 +362,13 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
     for (int j = 0; j < LOADS; ++j) {
       const int c = min(tid + THREADS * j, KT * DC - 1);
       const int key = min(kt + c / DC, L - 1);
-      r.k[j] = ldg128(kbase16 + (long)key * a.kss + 8 * (c % DC));
+      r.k[j] = kcol ? ldg128(kbase16 + (long)key * a.kss + 8 * (c % DC)) : zero4;
     }
     if (vthread) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = min(kt + 4 * vkq + j, L - 1);
-        r.v[j] = ldg128(vbase16 + (long)key * a.vss + 8 * vdc);
+        r.v[j] = vcol ? ldg128(vbase16 + (long)key * a.vss + 8 * vdc) : zero4;
       }
     }
   };
@@ -428,14 +441,14 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
         }
       }
       if (tid < KT) {
-        // 4-bit fields are staged as off + f: bias - off * scale takes the offset back out
+        // bf16 4-bit fields are staged as 128 + f: bias - 128 * scale takes the offset back out
 #pragma unroll
         for (int t = 0; t < 4; t += 2)
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             const float sc = to_f32<T>(r.sb[t * G + g]), bi = to_f32<T>(r.sb[(t + 1) * G + g]);
             qsb[bsel][t][g][tid] = sc;
-            qsb[bsel][t + 1][g][tid] = QB == 4 ? __builtin_fmaf(-kOff4<T>, sc, bi) : bi;
+            qsb[bsel][t + 1][g][tid] = (QB == 4 && kOff4<T> != 0.f) ? __builtin_fmaf(-kOff4<T>, sc, bi) : bi;
           }
       }
     } else {
@@ -711,7 +724,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
       u32x2_t pk2 = {pack2<T>(o[t][0] * inv, o[t][1] * inv), pack2<T>(o[t][2] * inv, o[t][3] * inv)};
-      *reinterpret_cast<u32x2_t*>(orow + 16 * t + 4 * q4) = pk2;
+      if (dbase + 16 * t + 4 * q4 < a.dv) *reinterpret_cast<u32x2_t*>(orow + 16 * t + 4 * q4) = pk2;
     }
     return;
   }
@@ -789,7 +802,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const AttnArgs a) {
 #pragma unroll
   for (int t = 0; t < DPL; ++t) so[wave][DPL * lane + t] = num[t];
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += 256) {
+  for (int d = threadIdx.x; d < a.dv; d += 256) {
     const float Mx = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
     float nn = 0.f, dd = 0.f;
 #pragma unroll

@@ -11,13 +11,16 @@ int check_shape(long B, long Hq, long Mq, long D, long Hk, long L) {
   if (B < 1 || Hq < 1 || Hk < 1 || Mq < 1 || L < 1)
     return fail(DSPARK_ERR_SHAPE, "verify_attention: B=%ld Hq=%ld Hk=%ld Mq=%ld L=%ld", B, Hq, Hk, Mq, L);
   if (Hq % Hk) return fail(DSPARK_ERR_SHAPE, "verify_attention: Hq=%ld not a multiple of Hk=%ld", Hq, Hk);
-  if (D != 64 && D != 128 && D != 256)
-    return fail(DSPARK_ERR_SHAPE, "verify_attention: head_dim %ld (64, 128 or 256 supported)", D);
+  if (D < 8 || D > 256 || D % 8)
+    return fail(DSPARK_ERR_SHAPE, "verify_attention: head_dim %ld (a multiple of 8 up to 256)", D);
   if (Mq > L) return fail(DSPARK_ERR_SHAPE, "verify_attention: Mq=%ld > L=%ld", Mq, L);
   if ((Hq / Hk) * Mq > 256) return fail(DSPARK_ERR_SHAPE, "verify_attention: gqa*Mq=%ld > 256", (Hq / Hk) * Mq);
   if (L >= (1L << 30) || B * Hk >= (1L << 20)) return fail(DSPARK_ERR_SHAPE, "verify_attention: too large");
   return DSPARK_OK;
 }
+
+// the kernel instance serving head dim D: 64, 128 or 256 columns, the missing ones zero
+long instance_d(long D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
 
 int check_strides(const int64_t* s, long mult, const char* what) {
   for (int i = 0; i < 3; ++i)
@@ -47,8 +50,9 @@ int prepare(const Common& c, AttnArgs& a, Plan& p) {
   if (c.tree_anc && c.Mq > 32) return fail(DSPARK_ERR_SHAPE, "verify_attention: tree mask needs Mq <= 32");
   if (!aligned(c.q, 16) || !aligned(c.out, 8))
     return fail(DSPARK_ERR_ALIGN, "verify_attention: q must be 16-byte aligned, out 8-byte aligned");
-  p = make_plan(c.B, c.Hq, c.Hk, c.Mq, c.D, c.L);
-  const size_t need = partial_bytes(p, c.B, c.Hk, c.D);
+  const long DI = instance_d(c.D);
+  p = make_plan(c.B, c.Hq, c.Hk, c.Mq, DI, c.L);
+  const size_t need = partial_bytes(p, c.B, c.Hk, DI);
   if (need && (!c.workspace || c.workspace_bytes < need))
     return fail(DSPARK_ERR_WORKSPACE, "verify_attention: workspace %zu < %zu bytes", c.workspace_bytes, need);
   if (need && !aligned(c.workspace, 16))
@@ -63,6 +67,7 @@ int prepare(const Common& c, AttnArgs& a, Plan& p) {
   a.Hk = (int)c.Hk;
   a.Mq = (int)c.Mq;
   a.L = (int)c.L;
+  a.dv = (int)c.D;
   a.gqa = (int)(c.Hq / c.Hk);
   a.R = p.R;
   a.RT = p.RT;
@@ -74,7 +79,7 @@ int prepare(const Common& c, AttnArgs& a, Plan& p) {
   if (need) {
     const size_t rows = (size_t)c.B * c.Hk * p.NB * p.RP;
     a.opart = static_cast<float*>(c.workspace);
-    a.mpart = a.opart + rows * c.D;
+    a.mpart = a.opart + rows * DI;
     a.lpart = a.mpart + rows;
   }
   return DSPARK_OK;
@@ -82,8 +87,9 @@ int prepare(const Common& c, AttnArgs& a, Plan& p) {
 
 template <class T>
 int launch_d(const AttnArgs& a, const Plan& p, long B, long D, bool tree, int qbits, hipStream_t s) {
-  if (D == 64) return launch<T, 64>(a, p, B, tree, qbits, s);
-  if (D == 128) return launch<T, 128>(a, p, B, tree, qbits, s);
+  const long DI = instance_d(D);
+  if (DI == 64) return launch<T, 64>(a, p, B, tree, qbits, s);
+  if (DI == 128) return launch<T, 128>(a, p, B, tree, qbits, s);
   return launch<T, 256>(a, p, B, tree, qbits, s);
 }
 
@@ -133,7 +139,8 @@ using namespace dspark::attn;
 extern "C" size_t dspark_verify_attention_workspace(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
                                                     int64_t L_total) {
   if (check_shape(B, Hq, Mq, D, Hk, L_total)) return 0;
-  return partial_bytes(make_plan(B, Hq, Hk, Mq, D, L_total), B, Hk, D);
+  const long DI = instance_d(D);
+  return partial_bytes(make_plan(B, Hq, Hk, Mq, DI, L_total), B, Hk, DI);
 }
 
 extern "C" int dspark_verify_attention_plan(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
@@ -141,7 +148,7 @@ extern "C" int dspark_verify_attention_plan(int64_t B, int64_t Hq, int64_t Hk, i
   if (!out) return fail(DSPARK_ERR_ARG, "verify_attention_plan: null output");
   const int st = check_shape(B, Hq, Mq, D, Hk, L_total);
   if (st) return st;
-  const Plan p = make_plan(B, Hq, Hk, Mq, D, L_total);
+  const Plan p = make_plan(B, Hq, Hk, Mq, instance_d(D), L_total);
   out[0] = p.R;
   out[1] = p.RP;
   out[2] = p.NRG;
@@ -154,7 +161,7 @@ extern "C" int dspark_verify_attention_plan(int64_t B, int64_t Hq, int64_t Hk, i
 extern "C" int64_t dspark_verify_attention_blocks(int64_t B, int64_t Hq, int64_t Hk, int64_t Mq, int64_t D,
                                                   int64_t L_total) {
   if (check_shape(B, Hq, Mq, D, Hk, L_total)) return -1;
-  return make_plan(B, Hq, Hk, Mq, D, L_total).NB;
+  return make_plan(B, Hq, Hk, Mq, instance_d(D), L_total).NB;
 }
 
 extern "C" int dspark_verify_attention_typed(int dtype, const void* q, int64_t B, int64_t Hq, int64_t Mq, int64_t D,
@@ -199,6 +206,8 @@ extern "C" int dspark_verify_attention_quantized(
   if (bits != 4 && bits != 8) return fail(DSPARK_ERR_UNSUPPORTED, "verify_attention_quantized: bits=%d (4 or 8)", bits);
   if (group_size != 64)
     return fail(DSPARK_ERR_UNSUPPORTED, "verify_attention_quantized: group_size=%d (64 supported)", group_size);
+  if (D != 64 && D != 128 && D != 256)
+    return fail(DSPARK_ERR_SHAPE, "verify_attention_quantized: head_dim %ld (64, 128 or 256)", (long)D);
   if (!k_words || !k_scales || !k_biases || !v_words || !v_scales || !v_biases || !k_strides || !v_strides ||
       !k_scale_strides || !v_scale_strides)
     return fail(DSPARK_ERR_ARG, "verify_attention_quantized: null pointer");

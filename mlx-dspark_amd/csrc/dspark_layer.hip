@@ -157,24 +157,27 @@ struct QkArgs {
   u16* vc;
   long ldq, ldk, ldv;
   long kch, kcs, vch, vcs;  // cache strides (head, position) in elements
-  int M, Hq, Hk, pos0;
+  int M, Hq, Hk, pos0, D;
   float eps, log2_base;
 };
 
-// one wave per (row, head); lane i < D/2 owns the RoPE pair (i, i + D/2)
-template <int D>
+// one wave per (row, head); lane l owns the RoPE pairs (i, i + D/2) for i = l + 64 j, j < NP
+// (NP = ceil(D / 128): head dims up to 128 take one pair per lane, up to 256 two)
+template <int NP>
 __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(const QkArgs a) {
-  constexpr int HALF = D / 2;
+  const int D = a.D, HALF = a.D >> 1;
   const int m = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
-  const bool on = lane < HALF;
-  const int i = on ? lane : 0;
   if (hh >= a.Hq + a.Hk) {  // V head: copy into the cache
     const int h = hh - a.Hq - a.Hk;
     const u16* src = a.v + (long)m * a.ldv + (long)h * D;
     u16* dst = a.vc + (long)h * a.vch + (long)(a.pos0 + m) * a.vcs;
-    if (on) {
-      dst[i] = src[i];
-      dst[i + HALF] = src[i + HALF];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int i = lane + 64 * j;
+      if (i < HALF) {
+        dst[i] = src[i];
+        dst[i + HALF] = src[i + HALF];
+      }
     }
     return;
   }
@@ -182,25 +185,31 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(const QkArgs a) {
   const int h = isq ? hh : hh - a.Hq;
   const u16* src = isq ? a.q + (long)m * a.ldq + (long)h * D : a.k + (long)m * a.ldk + (long)h * D;
   const u16* w = isq ? a.qw : a.kw;
-  const float x1 = on ? bf2f(src[i]) : 0.f, x2 = on ? bf2f(src[i + HALF]) : 0.f;
-  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  float x1[NP], x2[NP];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int i = lane + 64 * j;
+    const bool on = i < HALF;
+    x1[j] = on ? bf2f(src[i]) : 0.f;
+    x2[j] = on ? bf2f(src[i + HALF]) : 0.f;
+    ss += x1[j] * x1[j] + x2[j] * x2[j];
+  }
+  ss = wave_sum(ss);
   const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + a.eps);
-  const float n1 = bf16r(bf16r(x1 * inv) * bf2f(w[i]));
-  const float n2 = bf16r(bf16r(x2 * inv) * bf2f(w[i + HALF]));
-  const float inv_freq = exp2f(-(2.0f * (float)i / (float)D) * a.log2_base);
-  const float ang = (float)(a.pos0 + m) * inv_freq;
-  float sn, cs;
-  sincosf(ang, &sn, &cs);
-  const u16 o1 = f2bf(n1 * cs - n2 * sn), o2 = f2bf(n1 * sn + n2 * cs);
-  if (!on) return;
-  if (isq) {
-    u16* dst = a.qout + ((long)h * a.M + m) * D;
-    dst[i] = o1;
-    dst[i + HALF] = o2;
-  } else {
-    u16* dst = a.kc + (long)h * a.kch + (long)(a.pos0 + m) * a.kcs;
-    dst[i] = o1;
-    dst[i + HALF] = o2;
+  u16* dst = isq ? a.qout + ((long)h * a.M + m) * D : a.kc + (long)h * a.kch + (long)(a.pos0 + m) * a.kcs;
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int i = lane + 64 * j;
+    if (i >= HALF) break;
+    const float n1 = bf16r(bf16r(x1[j] * inv) * bf2f(w[i]));
+    const float n2 = bf16r(bf16r(x2[j] * inv) * bf2f(w[i + HALF]));
+    const float inv_freq = exp2f(-(2.0f * (float)i / (float)D) * a.log2_base);
+    const float ang = (float)(a.pos0 + m) * inv_freq;
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    dst[i] = f2bf(n1 * cs - n2 * sn);
+    dst[i + HALF] = f2bf(n1 * sn + n2 * cs);
   }
 }
 
@@ -347,8 +356,9 @@ __global__ __launch_bounds__(kAaThreads) void argmax_accept_kernel(const u16* __
     for (int w = 1; w < kAaThreads / 64; ++w) arg_better(b, id, sv[w], si[w]);
     __hip_atomic_store(&pval[m * C + c], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&pidx[m * C + c], id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): both stores are complete before the arrival
-    last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == C * M - 1;
+    // release: this chunk's result is visible before the arrival; acquire: the last arriver
+    // sees every other chunk's (the workgroup barrier below extends it to the other threads)
+    last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == C * M - 1;
   }
   __syncthreads();
   if (!last) return;
@@ -431,7 +441,8 @@ extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k,
                                       const int64_t v_cache_strides[2], dspark_stream stream) {
   if (!q || !k || !v || !q_norm_w || !k_norm_w || !q_out || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides)
     return fail(DSPARK_ERR_ARG, "qk_norm_rope_kv: null pointer");
-  if (D != 64 && D != 128) return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: head_dim %lld (64 or 128)", (long long)D);
+  if (D < 8 || D > 256 || D % 8)
+    return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: head_dim %lld (a multiple of 8 up to 256)", (long long)D);
   if (M < 1 || M > 65535 || Hq < 1 || Hk < 1 || Hq + 2 * Hk > 65535 || pos0 < 0 || pos0 + M > (1L << 30))
     return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: M=%lld Hq=%lld Hk=%lld pos0=%lld", (long long)M, (long long)Hq,
                 (long long)Hk, (long long)pos0);
@@ -457,12 +468,13 @@ extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k,
   a.Hq = (int)Hq;
   a.Hk = (int)Hk;
   a.pos0 = (int)pos0;
+  a.D = (int)D;
   a.eps = eps;
   a.log2_base = log2f(rope_base);
   const dim3 grid((unsigned)M, (unsigned)(Hq + 2 * Hk));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 128) hipLaunchKernelGGL(qk_norm_rope_kv_kernel<128>, grid, dim3(64), 0, s, a);
-  else hipLaunchKernelGGL(qk_norm_rope_kv_kernel<64>, grid, dim3(64), 0, s, a);
+  if (D <= 128) hipLaunchKernelGGL(qk_norm_rope_kv_kernel<1>, grid, dim3(64), 0, s, a);
+  else hipLaunchKernelGGL(qk_norm_rope_kv_kernel<2>, grid, dim3(64), 0, s, a);
   return check_launch("qk_norm_rope_kv");
 }
 

@@ -756,3 +756,17 @@ extern "C" int dspark_qmm_affine_noalloc(const void* x, int64_t ldx, int64_t M, 
   if (need && (st = scratch_for_current_device(s, &ptr))) return st;
   return multi_impl(&p, 1, M, bits, group_size, false, ptr, need ? kNoallocBytes : 0, s);
 }
+
+extern "C" int dspark_qmm_noalloc_reset(dspark_stream stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ptr = nullptr;
+  const int st = scratch_for_current_device(s, &ptr);
+  if (st) return st;
+  return zero_counters(ptr, kCtrRegionBytes, s, "dspark_qmm_noalloc_reset");
+}
+
+extern "C" int dspark_qmm_noalloc_scratch(void** ptr, size_t* bytes) {
+  if (!ptr || !bytes) return fail(DSPARK_ERR_ARG, "qmm_noalloc_scratch: null pointer");
+  *bytes = kNoallocBytes;
+  return scratch_for_current_device(nullptr, ptr);
+}

@@ -91,6 +91,8 @@ SIGNATURES: dict[str, tuple] = {
                                       c_void_p, c_i64, c_void_p]),
     "dspark_qmm_affine_noalloc": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_i64,
                                           c_int, c_int, c_void_p, c_i64, c_void_p]),
+    "dspark_qmm_noalloc_reset": (c_int, [c_void_p]),
+    "dspark_qmm_noalloc_scratch": (c_int, [ctypes.POINTER(c_void_p), ctypes.POINTER(c_size_t)]),
     "dspark_qmm_affine_supported": (c_int, [c_i64, c_i64, c_i64, c_int, c_int]),
     "dspark_qmm_affine_plan": (c_int, [c_i64, c_i64, c_i64, c_int, c_int, ctypes.POINTER(ctypes.c_int32)]),
     "dspark_qmm_affine_multi": (c_int, [ctypes.POINTER(QmmProblem), c_int, c_i64, c_int, c_int, c_void_p,

@@ -158,16 +158,35 @@ class DenseModel(nn.Module):
         return [KVCache(1, a.num_key_value_heads, a.head_dim, device=dev, capacity=capacity)
                 for _ in range(a.num_hidden_layers)]
 
-    def body(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
-        """ids [1, L] -> final-normed hidden states [1, L, H] (the module path)."""
+    def body(self, ids: torch.Tensor, cache: list[KVCache], tap=None):
+        """ids [1, L] -> (final-normed hidden states [1, L, H], fused | None), the module path.
+        ``fused`` [1, L, n_tap * H] concatenates the residual stream after every decoder layer
+        whose index is in ``tap``, in layer order (target.py:208-220 ``_body_mlxlm``); ``tap``
+        None skips the capture."""
+        slots = tap_layers(tap, len(self.layers))
         h = self.embed_tokens[ids]
-        for layer, c in zip(self.layers, cache):
+        captured = []
+        for i, (layer, c) in enumerate(zip(self.layers, cache)):
             h = layer(h, c)
-        return rms_norm(h, self.norm, self.args.rms_norm_eps)
+            if i in slots:
+                captured.append(h)
+        fused = None
+        if tap is not None:
+            fused = torch.cat(captured, dim=-1) if captured else h.new_empty((*h.shape[:-1], 0))
+        return rms_norm(h, self.norm, self.args.rms_norm_eps), fused
 
     def forward(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
         """ids [1, L] -> logits [1, L, V] (the module path)."""
-        return self.lm_head(self.body(ids, cache))
+        return self.lm_head(self.body(ids, cache)[0])
+
+
+def tap_layers(tap, n_layers: int) -> tuple[int, ...]:
+    """The layers a hidden-state tap captures, in layer order: the reference tests each layer
+    index against the tap set while it walks the stack (target.py:210-219), so the order of
+    ``tap``, duplicates and indices outside the stack do not matter."""
+    if tap is None:
+        return ()
+    return tuple(sorted({int(i) for i in tap if 0 <= int(i) < n_layers}))
 
 
 PREFILL_CHUNK = 2048    # a long prompt prefills in pieces of this many rows (generate.py:1026)
@@ -222,6 +241,10 @@ class VerifyEngine:
         self.qmm_ws = ops.new_qmm_workspace(dev, self._qmm_workspace_need())
         self.accept_ws = torch.zeros(max(ops.argmax_accept_workspace_bytes(max_rows, a.vocab_size), 256),
                                      dtype=torch.uint8, device=dev)
+        # hidden-state tap: the residual stream after each tapped layer, written in place by the
+        # residual add that forms it (no copy), [max_rows, n_tap * H]; see set_tap
+        self.tap: tuple[int, ...] = ()
+        self.fused = e(max_rows, 0)
         self.attn_ws = torch.empty(max(ops.attention_workspace_bound(1, hq, hk, d, max_rows), 16), dtype=torch.uint8,
                                    device=dev)
 
@@ -243,6 +266,17 @@ class VerifyEngine:
         need.append(ops.qmm_launch_workspace_bytes(M, a.hidden_size, [lm.weight.shape[0]], lm.bits))
         return max(need)
 
+    def set_tap(self, tap) -> tuple[int, ...]:
+        """Select the layers whose residual-stream output the step writes into ``self.fused``
+        (column block j holds layer ``self.tap[j]``). Reallocates the buffer when the number of
+        tapped layers changes, so call it before capturing a step in a graph."""
+        slots = tap_layers(tap, self.args.num_hidden_layers)
+        if len(slots) != self.fused.shape[1] // self.args.hidden_size:
+            self.fused = torch.empty((self.max_rows, len(slots) * self.args.hidden_size), dtype=torch.bfloat16,
+                                     device=self.h.device)
+        self.tap = slots
+        return slots
+
     def _qmm(self, x: torch.Tensor, mods, outs) -> None:
         """One launch of ``x @ W^T`` for the modules ``mods`` (same K and bits) into ``outs``."""
         packs = [self._packed.get(id(mod)) for mod in mods]
@@ -256,22 +290,35 @@ class VerifyEngine:
     def step(self, M: int, cache: list[KVCache], pos0: int, *, accept: bool = False) -> torch.Tensor:
         """Run the forward over ``self.ids[:M]`` at cache positions pos0..pos0+M-1 (caches
         already reserved); logits in ``self.logits[:M]``; with ``accept``, also the target
-        tokens ``self.tt[:M]`` and the accepted count ``self.n_acc`` for ``self.draft[:M-1]``.
+        tokens ``self.tt[:M]`` and the accepted count ``self.n_acc`` for ``self.draft[:M-1]``;
+        the tapped layers' residual streams (``set_tap``) in ``self.fused[:M]``.
         Enqueues kernels only (graph-capturable for a fixed pos0)."""
         a, m = self.args, self.model
         hq, hk, d, eps = a.num_attention_heads, a.num_key_value_heads, a.head_dim, a.rms_norm_eps
         h, r, y = self.h[:M], self.r[:M], self.y[:M]
         torch.index_select(m.embed_tokens, 0, self.ids[:M], out=h)
         L = pos0 + M
+        H = a.hidden_size
+        slot = {li: j for j, li in enumerate(self.tap)}
+
+        def stream_out(li: int) -> torch.Tensor:
+            """Where the residual add that completes layer ``li`` writes the stream: its tap
+            column block when tapped (the next add reads it from there), else ``h``."""
+            j = slot.get(li)
+            return h if j is None else self.fused[:M, j * H:(j + 1) * H]
+
+        hcur = h
         qatt = self.qatt[:, :, :M]
         if M != self.max_rows:
             qatt = self.qatt.view(-1)[:hq * M * d].view(1, hq, M, d)
         for li, (layer, c) in enumerate(zip(m.layers, cache)):
             at, mlp = layer.self_attn, layer.mlp
             if li == 0:
-                ops.rmsnorm(h, layer.input_layernorm, eps, out=y)
+                ops.rmsnorm(hcur, layer.input_layernorm, eps, out=y)
             else:
-                ops.rmsnorm(h, layer.input_layernorm, eps, residual=r, h_out=h, out=y)
+                dst = stream_out(li - 1)
+                ops.rmsnorm(hcur, layer.input_layernorm, eps, residual=r, h_out=dst, out=y)
+                hcur = dst
             self._qmm(y, [at.q_proj, at.k_proj, at.v_proj], [self.q[:M], self.k[:M], self.v[:M]])
             ops.qk_norm_rope_kv(self.q[:M], self.k[:M], self.v[:M], at.q_norm, at.k_norm, heads=hq, kv_heads=hk,
                                 head_dim=d, eps=eps, rope_base=a.rope_theta, pos0=pos0, q_out=qatt[0],
@@ -281,7 +328,8 @@ class VerifyEngine:
             ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1,
                                       workspace=self.attn_ws)
             self._qmm(att, [at.o_proj], [r])
-            ops.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
+            ops.rmsnorm(hcur, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
+            hcur = h
             pair = self._swiglu.get(id(mlp))
             if pair is not None:
                 ops.quantized_swiglu_packed(y, pair, out=self.hm[:M], workspace=self.qmm_ws)
@@ -289,7 +337,7 @@ class VerifyEngine:
                 self._qmm(y, [mlp.gate_proj, mlp.up_proj], [self.g[:M], self.u[:M]])
                 ops.swiglu(self.g[:M], self.u[:M], out=self.hm[:M])
             self._qmm(self.hm[:M], [mlp.down_proj], [r])
-        ops.rmsnorm(h, m.norm, eps, residual=r, h_out=h, out=y)
+        ops.rmsnorm(hcur, m.norm, eps, residual=r, h_out=stream_out(len(m.layers) - 1), out=y)
         lm = m.lm_head
         logits = self.logits[:M]
         self._qmm(y, [lm], [logits])
@@ -310,13 +358,23 @@ class Target:
     def make_cache(self, capacity: int = 0) -> list[KVCache]:
         return self.model.make_cache(capacity)
 
+    def _fused_rows(self, M: int, tap):
+        """The step's tap output as the reference returns it: [1, M, n_tap * H], or None."""
+        if tap is None:
+            return None
+        return self.engine.fused[:M].reshape(1, M, -1)
+
     def verify(self, ids: torch.Tensor, cache: list[KVCache], tap=None):
-        """ids [1, 1+m] = [anchor] + m drafts -> (logits [1, 1+m, V], None). Writes the rows
-        into every layer's cache (offset advances by 1+m)."""
+        """ids [1, 1+m] = [anchor] + m drafts -> (logits [1, 1+m, V], fused [1, 1+m, n_tap*H]),
+        the residual stream after each tapped layer, in layer order (target.py:642-677,
+        :208-220); ``tap=None`` skips the capture and returns ``fused=None``. Writes the rows
+        into every layer's cache (offset advances by 1+m). Both results are views of the
+        engine's buffers, valid until its next step."""
         flat = ids.reshape(-1)
         M = int(flat.numel())
         if not 1 <= M <= self.max_rows:
             raise ValueError(f"verify width {M} outside 1..{self.max_rows}")
+        self.engine.set_tap(tap)
         for c in cache:
             c.reserve(M)
         pos0 = cache[0].offset
@@ -324,32 +382,28 @@ class Target:
         logits = self.engine.step(M, cache, pos0)
         for c in cache:
             c.advance(M)
-        return logits.reshape(1, M, -1), None
+        return logits.reshape(1, M, -1), self._fused_rows(M, tap)
 
-    def prefill(self, ids: torch.Tensor, cache: list[KVCache], *, chunk: int | None = None,
-                head_last_row: bool = True) -> torch.Tensor:
-        """Fill the caches with a prompt before the verify loop: module-path forwards of at most
-        ``chunk`` rows (default :data:`PREFILL_CHUNK`), under the prefill wide path the
-        process has configured (``calibrate.apply_wide_gemm``; bit-identical to the stock path
-        by its gate), then the head over the last row only (``head_last_row``) or every row of
-        the final chunk. Returns logits [1, 1 or rows, V] (generate.py:1073-1100,
-        target.py:435-465)."""
-        from . import calibrate
-        from .wide_gemm import wide_matmul
+    def run(self, ids: torch.Tensor, cache: list[KVCache], tap):
+        """ids [1, L] -> (logits [1, L, V], fused [1, L, n_tap*H] | None) through the module
+        path (target.py:187-197 ``run``, the mlx-lm branch)."""
+        hn, fused = self.model.body(ids.reshape(1, -1).to(self.model.embed_tokens.device, torch.int64), cache, tap)
+        return self.model.lm_head(hn), fused
 
+    def prefill(self, ids: torch.Tensor, cache: list[KVCache], tap=None, *, want_logits: bool = False,
+                head_last_row: bool = True):
+        """One prefill chunk -> ``(logits | None, fused | None)`` (target.py:435-465): the module
+        path over ``ids`` [1, L] writing the caches, the tapped hidden states when ``tap`` is
+        given, and the vocab projection only with ``want_logits`` (of the last row alone with
+        ``head_last_row``). It runs under whatever projection scope is active;
+        :func:`prefill_plain` chunks a prompt under the prefill wide path."""
         flat = ids.reshape(1, -1).to(self.model.embed_tokens.device, torch.int64)
-        L = int(flat.shape[1])
-        if L == 0:
-            raise ValueError("prefill: empty prompt")
-        chunk = int(chunk or PREFILL_CHUNK)
-        with wide_matmul(calibrate.WIDE_GEMM_MIN_ROWS, calibrate.WIDE_GEMM_SHAPES):
-            hn = None
-            for i in range(0, L, chunk):
-                hn = self.model.body(flat[:, i:i + chunk], cache)
-            return self.model.lm_head(hn[:, -1:] if head_last_row else hn)
-
-    def plain(self, ids: torch.Tensor, cache: list[KVCache]) -> torch.Tensor:
-        return self.verify(ids, cache)[0]
+        if flat.shape[1] == 0:
+            raise ValueError("prefill: empty chunk")
+        hn, fused = self.model.body(flat, cache, tap)
+        if not want_logits:
+            return None, fused
+        return self.model.lm_head(hn[:, -1:] if head_last_row else hn), fused
 
     def rollback(self, cache: list[KVCache], n_rejected: int, accepted=None) -> None:
         """Dense rollback: trim every cache by the rejected rows; 0 is a no-op."""
@@ -358,14 +412,18 @@ class Target:
                 if c is not None and hasattr(c, "trim"):
                     c.trim(n_rejected)
 
-    def greedy_round(self, pending: int, draft: list[int], cache: list[KVCache]) -> tuple[int, list[int]]:
+    def greedy_round(self, pending: int, draft: list[int], cache: list[KVCache], tap=None):
         """One speculative round (generate.py:1544-1593): verify [pending] + draft, argmax and
         accept on the device, one host read, rollback of the rejected rows. Returns
-        (n accepted drafts, committed tokens = accepted drafts + the target's bonus token)."""
+        (n accepted drafts, committed tokens = accepted drafts + the target's bonus token,
+        context rows): the context rows are ``fused[:, :n + 1]``, the tapped hidden states of
+        [pending, accepted drafts] the drafter's ``update_context`` takes (generate.py:1590-1593),
+        or None without a tap."""
         e = self.engine
         M = 1 + len(draft)
         if M > self.max_rows:
             raise ValueError(f"verify width {M} > {self.max_rows}")
+        e.set_tap(tap)
         for c in cache:
             c.reserve(M)
         pos0 = cache[0].offset
@@ -378,7 +436,33 @@ class Target:
         tt = e.tt[:M].tolist()                    # the round's one host read
         n = int(e.n_acc.item()) if draft else 0
         self.rollback(cache, len(draft) - n)
-        return n, list(draft[:n]) + [int(tt[n])]
+        fused = self._fused_rows(M, tap)
+        return n, list(draft[:n]) + [int(tt[n])], None if fused is None else fused[:, :n + 1]
+
+
+def prefill_plain(target: Target, ids: torch.Tensor, cache: list[KVCache], chunk: int | None = None,
+                  tap=None):
+    """Chunked prefill of a prompt before the verify loop (generate.py:1073-1100
+    ``_prefill_plain``): pieces of at most ``chunk`` rows (default :data:`PREFILL_CHUNK`) under
+    the prefill wide path the process has configured (``calibrate.apply_wide_gemm``,
+    bit-identical to the stock path by its gate), the vocab projection of the last row of the
+    last piece only. Returns (logits [1, 1, V], fused of the whole prompt | None)."""
+    from . import calibrate
+    from .wide_gemm import wide_matmul
+
+    flat = ids.reshape(1, -1)
+    L = int(flat.shape[1])
+    if L == 0:
+        raise ValueError("prefill: empty prompt")
+    chunk = int(chunk or PREFILL_CHUNK)
+    logits, pieces = None, []
+    with wide_matmul(calibrate.WIDE_GEMM_MIN_ROWS, calibrate.WIDE_GEMM_SHAPES):
+        for i in range(0, L, chunk):
+            last = i + chunk >= L
+            logits, fused = target.prefill(flat[:, i:i + chunk], cache, tap, want_logits=last, head_last_row=True)
+            if fused is not None:
+                pieces.append(fused)
+    return logits, (torch.cat(pieces, dim=1) if pieces else None)
 
 
 def greedy_generate(target: Target, prompt: list[int], steps: int) -> list[int]:

@@ -4,8 +4,9 @@ its scoped patch of the attention entry points (plain and quantized-cache).
 Same API as the reference module (multirow_attn.py:204-488): ``plan``, ``multirow_sdpa``,
 ``Window``, ``MultirowConfig``, ``eligible``, ``tree_mask``, ``multirow_attention``,
 ``active`` and ``measure_window``. The kernel is ``dspark_verify_attention_typed`` (split-KV
-pass plus combine, v_mfma_f32_16x16x32_{bf16,f16}); it serves bf16 and fp16, head_dim 64, 128
-or 256 (the reference's D <= 256, multirow_attn.py:200-214, :294-307), whole GQA groups with
+pass plus combine, v_mfma_f32_16x16x32_{bf16,f16}); it serves bf16 and fp16, any head_dim
+d % 8 == 0 up to 256 (the reference's rule, multirow_attn.py:200-214, :294-307; instances at 64,
+128 and 256, smaller head dims zero-padded on chip), whole GQA groups with
 gqa * q_len <= 256, and reads K/V through their batch/head/sequence strides (KV-cache views
 sliced along the sequence axis are used in place). ``quantized_sdpa`` runs the same kernel
 over mlx-lm's quantized-cache triples (``dspark_verify_attention_quantized``).
@@ -34,7 +35,6 @@ from . import _lib, _scope, fast, gate, ops
 _STOCK = fast.STOCK
 
 MAX_D = 256
-HEAD_DIMS = ops.ATTN_HEAD_DIMS
 MAX_ROWS = 256          # gqa * q_len the kernel's row tiles cover
 _DTYPES = tuple(ops.ATTN_DTYPES)
 
@@ -111,7 +111,7 @@ def why_not(q, k, v, mask, sinks, cfg: MultirowConfig) -> str | None:
         return "kv_len below the window"
     if not (q.dtype in _DTYPES and k.dtype == v.dtype == q.dtype):
         return "dtype"
-    if D not in HEAD_DIMS or k.shape[-1] != D or v.shape[-1] != D:
+    if not ops.attn_head_dim_ok(D) or k.shape[-1] != D or v.shape[-1] != D:
         return "head_dim"
     if Hk == 0 or Hq % Hk or tuple(v.shape[:3]) != (B, Hk, L) or k.shape[0] != B:
         return "heads"
@@ -167,20 +167,34 @@ def _route(q, k, v, scale, mask, sinks, cfg):
 
 def why_not_quantized(q, q_keys, q_values, mask, cfg: MultirowConfig, group_size: int, bits: int) -> str | None:
     """:func:`why_not` for a quantized-cache call: the same window and shape rules, on the
-    (words, scales, biases) triples."""
+    (words, scales, biases) triples, plus the triples' own layout (every shape, unit last
+    strides, scales and biases sharing strides), so a malformed triple falls through to the
+    stock path instead of raising inside the scope."""
     if bits not in ops.KV_BITS or group_size != 64:
         return "format"
     kw, ks, kb = q_keys
     vw, vs, vb = q_values
-    if not (kw.dim() == vw.dim() == ks.dim() == 4):
+    if not all(t.dim() == 4 for t in (kw, ks, kb, vw, vs, vb)) or q.dim() != 4:
         return "rank"
-    D = q.shape[-1] if q.dim() == 4 else 0
+    D = q.shape[-1]
+    if D not in ops.QUANT_HEAD_DIMS:
+        return "head_dim"
     k_like = torch.empty((kw.shape[0], kw.shape[1], kw.shape[2], D), dtype=ks.dtype, device="meta")
     reason = why_not(q, k_like, k_like, mask, None, cfg)
     if reason:
         return reason
+    lead = tuple(kw.shape[:3])
     if kw.shape[-1] * 32 // bits != D or tuple(vw.shape) != tuple(kw.shape):
         return "head_dim"
+    G = D // group_size
+    if any(tuple(t.shape) != lead + (G,) for t in (ks, kb, vs, vb)):
+        return "scales"
+    if any(t.stride(-1) != 1 for t in (kw, ks, kb, vw, vs, vb)):
+        return "last-dim stride"
+    if ks.stride() != kb.stride() or vs.stride() != vb.stride():
+        return "scale/bias strides"
+    if any(t.dtype not in (torch.int32, torch.uint32) for t in (kw, vw)):
+        return "word dtype"
     if not (ks.dtype == kb.dtype == vs.dtype == vb.dtype == q.dtype):
         return "dtype"
     return None
@@ -258,7 +272,7 @@ def measure_window(hq: int, hk: int, d: int, *, dtype=torch.bfloat16, device="cu
     reference must stay within twice the stock path's plus 2e-3, or the shape is refused; the
     kernel wins a probe when the stock path takes more than ``WIN`` times as long (HIP-event
     chains over three KV sets). ``window`` is None when nothing wins or the kernel cannot run."""
-    if d not in HEAD_DIMS or hk == 0 or hq % hk or dtype not in _DTYPES:
+    if not ops.attn_head_dim_ok(d) or hk == 0 or hq % hk or dtype not in _DTYPES:
         return None, {"reason": "shape"}
     scale = d ** -0.5
     report: dict = {"shape": f"{hq}x{hk}x{d}", "points": {}}

@@ -93,7 +93,9 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
 def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = GROUP, bits: int = 4,
                            outs=None, workspace: torch.Tensor | None = None) -> list[torch.Tensor]:
     """Several ``quantized_matmul`` with the same M, K and bits in ONE launch (q/k/v; gate/up).
-    Bitwise equal to separate calls."""
+    Bitwise equal to separate calls, except that an 8-bit [4096, 4096] matrix (which alone takes
+    the whole-K kernel) may differ by an fp32 rounding of a bias term when one group of 64 x
+    values spans many binades (its per-group sums of x are then not exact in fp32)."""
     cnt = len(w_list)
     if not 1 <= cnt <= _lib.MAX_QMM_PROBLEMS:
         raise ValueError(f"1..{_lib.MAX_QMM_PROBLEMS} problems per launch, got {cnt}")
@@ -389,7 +391,13 @@ def _pick(ws: torch.Tensor | None, device, nbytes: int, qmm: bool):
 
 # ---------------------------------------------------------------------------- verify attention
 
-ATTN_HEAD_DIMS = (64, 128, 256)
+ATTN_HEAD_DIMS = (64, 128, 256)   # kernel instances; any head dim d % 8 == 0, d <= 256 runs on the next one up
+QUANT_HEAD_DIMS = (64, 128, 256)  # quantized caches: whole groups of 64 along the head dim
+
+
+def attn_head_dim_ok(d: int) -> bool:
+    """The reference's head-dim rule (multirow_attn.py:200, :306): d % 8 == 0 and d <= 256."""
+    return 8 <= d <= 256 and d % 8 == 0
 ATTN_DTYPES = {torch.bfloat16: 0, torch.float16: 1}   # dspark_dtype codes
 KV_BITS = (4, 8)
 
@@ -425,7 +433,7 @@ def verify_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale
                      tree_anc: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """``softmax(scale * q k^T + mask) v`` for few verify rows over a (strided) KV cache view.
 
-    q bf16 or fp16 [B, Hq, Mq, D] (D in 64, 128, 256); k/v of q's dtype [B, Hk, L, D] with unit
+    q bf16 or fp16 [B, Hq, Mq, D] (D % 8 == 0, D <= 256); k/v of q's dtype [B, Hk, L, D] with unit
     stride along D (any batch/head/seq strides, e.g. a ``[..., :L, :]`` slice of a larger
     cache). ``causal``: row i sees keys ``0 .. L - Mq + i``. ``tree_anc`` (uint32/int32 [Mq])
     selects the tree-verify mask.
@@ -475,6 +483,8 @@ def verify_attention_quantized(q: torch.Tensor, keys, values, *, scale: float, c
     for t in (kw, vw):
         _require_packed(t)
     B, Hq, mq, D = q.shape
+    if D not in QUANT_HEAD_DIMS:
+        raise ValueError(f"quantized caches: head_dim {D} (64, 128 or 256)")
     Hk, L = kw.shape[1], kw.shape[2]
     W, G = D * bits // 32, D // group_size
     for name, t, last in (("key words", kw, W), ("value words", vw, W), ("key scales", ks, G), ("key biases", kb, G),

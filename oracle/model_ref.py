@@ -89,9 +89,13 @@ class DenseRef:
         self.v = [np.asarray(v, np.float32) for v in values]
         self.offset = self.k[0].shape[1]
 
-    def forward(self, ids) -> np.ndarray:
-        """ids [M] at positions offset..offset+M-1 -> logits [M, V]; appends to the caches."""
+    def forward(self, ids, tap=None) -> np.ndarray:
+        """ids [M] at positions offset..offset+M-1 -> logits [M, V]; appends to the caches.
+        With ``tap`` (layer indices), ``self.fused`` [M, n_tap * H] holds the residual stream
+        after each tapped layer, in layer order (target.py:208-220 ``_body_mlxlm``)."""
         c = self.cfg
+        tapset = {int(i) for i in tap} if tap is not None else set()
+        captured = []
         M = len(ids)
         Hq, Hk, D, eps = c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
         pos = np.arange(self.offset, self.offset + M)
@@ -101,6 +105,8 @@ class DenseRef:
         for li, L in enumerate(self.layers):
             if r is not None:
                 h = bf(h + r)
+                if li - 1 in tapset:
+                    captured.append(h)
             y = rmsnorm(h, L["input_norm"], eps)
             q = qmm(y, L["q"]).reshape(M, Hq, D).transpose(1, 0, 2)
             k = qmm(y, L["k"]).reshape(M, Hk, D).transpose(1, 0, 2)
@@ -115,6 +121,9 @@ class DenseRef:
             y2 = rmsnorm(h, L["post_norm"], eps)
             r = qmm(swiglu(qmm(y2, L["gate"]), qmm(y2, L["up"])), L["down"])
         h = bf(h + r)
+        if len(self.layers) - 1 in tapset:
+            captured.append(h)
+        self.fused = np.concatenate(captured, axis=-1) if captured else np.zeros((M, 0), np.float32)
         self.offset += M
         return qmm(rmsnorm(h, self.norm, eps), self.lm_head)
 

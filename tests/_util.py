@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from oracle.quant_ref import bf16_bits, bf16_from_bits, bf16_round
@@ -50,3 +52,28 @@ def assert_rms_close(got, ref, tol: float = 2e-2, what: str = ""):
     err, r = max_abs(got, ref), rms(ref)
     assert err <= tol * r, f"{what}: max|err| {err:.4g} > {tol} * RMS {r:.4g}"
     return err, r
+
+
+ROPE_KAT_P = (1, 17, 16384)
+# bf16 output rounding (2^-9 relative) plus the fp32 angle at p = 16384 (~1e-3 rad)
+ROPE_KAT_TOL = 4e-3
+
+
+def rope_kat_errors(rope_fn, D: int, base: float) -> float:
+    """Largest deviation of ``rope_fn(x [1, 1, D], pos [1], base)`` from the closed form of
+    non-traditional RoPE (dflash_model.py:187-194, ``traditional=False``): the unit vector e_i
+    (i < D/2) at position p becomes cos(p*theta_i) e_i + sin(p*theta_i) e_{i+D/2},
+    theta_i = base^(-2i/D), every other coordinate 0. i in {0, 1, D/4, D/2 - 1}, p in
+    ``ROPE_KAT_P``; the angles come from float64 ``math``, independent of the oracle."""
+    worst = 0.0
+    for i in sorted({0, 1, D // 4, D // 2 - 1}):
+        x = np.zeros((1, 1, D), np.float32)
+        x[..., i] = 1.0
+        theta = base ** (-2.0 * i / D)
+        for p in ROPE_KAT_P:
+            y = np.asarray(rope_fn(x, [p], base), np.float64).reshape(D)
+            want = np.zeros(D)
+            want[i] = math.cos(p * theta)
+            want[i + D // 2] = math.sin(p * theta)
+            worst = max(worst, float(np.abs(y - want).max()))
+    return worst

@@ -42,7 +42,9 @@ def test_shape_queries_without_gpu():
     assert lib.dspark_qmm_affine_supported(16, 4000, 4096, 4, 64) == -2
     assert lib.dspark_verify_attention_workspace(1, 32, 8, 16, 128, 32784) > 0
     assert lib.dspark_verify_attention_blocks(1, 32, 8, 16, 128, 32784) > 1
-    assert lib.dspark_verify_attention_blocks(1, 32, 8, 16, 96, 1024) == -1   # unsupported head_dim
+    assert lib.dspark_verify_attention_blocks(1, 32, 8, 16, 100, 1024) == -1  # head_dim % 8 != 0
+    assert lib.dspark_verify_attention_blocks(1, 32, 8, 16, 96, 1024) == \
+        lib.dspark_verify_attention_blocks(1, 32, 8, 16, 128, 1024)            # the 128-column instance
     assert lib.dspark_moe_workspace(16, 2048, 768, 128, 8) > 0
     assert lib.dspark_moe_workspace(16, 2048, 768, 128, 64) == 0              # k > 32
     assert lib.dspark_last_error() is not None

@@ -100,6 +100,50 @@ def test_head_dim_256_tree(dev):
     assert_rms_close(out, attn_ref.attention(q, k, v, 256 ** -0.5, tree_anc=anc), 2e-2, "D=256 tree")
 
 
+ODD_D = [
+    # d, B, hq, hk, q_len, L, causal: every head dim d % 8 == 0 up to 256 runs on the instance
+    # above it (64, 128, 256) with the missing columns zero; strided views over a wider cache
+    (8, 1, 8, 2, 5, 300, True),
+    (40, 2, 8, 8, 3, 129, True),
+    (72, 1, 32, 8, 16, 2064, True),      # 4-wave workgroups, split-KV blocks
+    (96, 1, 64, 8, 16, 1500, True),      # 128 rows per KV head: 8-wave workgroups
+    (112, 1, 32, 8, 16, 600, True),      # short cache: key-split workgroups
+    (160, 1, 16, 8, 16, 1000, False),    # instance 256, non-causal
+    (192, 1, 24, 4, 16, 3000, True),     # instance 256, 96 rows: 6-tile workgroups
+    (248, 1, 4, 1, 3, 23, True),         # tail shorter than a tile
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("d,B,hq,hk,q_len,L,causal", ODD_D)
+def test_any_head_dim_multiple_of_8(dev, dt, d, B, hq, hk, q_len, L, causal):
+    q, k, v = _mk(d * 3 + L, B, hq, hk, q_len, L, d, dt=dt, slack=13)
+    out = _run(dev, q, k, v, L, d ** -0.5, causal, dt=dt)
+    ref = attn_ref.attention(q, k[:, :, :L], v[:, :, :L], d ** -0.5, causal=causal)
+    assert_rms_close(out, ref, 2e-2, f"{dt} D={d} {hq}/{hk} q{q_len} L{L}")
+
+
+def test_any_head_dim_tree_and_strided_out(dev):
+    """Head dim 80 under a tree mask, written through the o-projection layout [B, Mq, Hq*D]:
+    only the caller's 80 columns of each head are written (the bytes between stay untouched)."""
+    from dspark_rocm import ops
+
+    d, hq, hk, mq, L = 80, 16, 4, 12, 700
+    q, k, v = _mk(80, 1, hq, hk, mq, L, d)
+    r = np.random.Generator(np.random.PCG64(9))
+    anc = [1]
+    for i in range(1, mq):
+        anc.append(anc[int(r.integers(0, i))] | (1 << i))
+    ref = attn_ref.attention(q, k, v, d ** -0.5, tree_anc=anc)
+    rows = torch.full((1, mq, hq * d + 8), 7.0, dtype=torch.bfloat16, device=dev)
+    ops.verify_attention_into(_dev(q, "bf16", dev), _dev(k, "bf16", dev), _dev(v, "bf16", dev), rows,
+                              (mq * (hq * d + 8), d, hq * d + 8), scale=d ** -0.5, causal=False,
+                              tree_anc=torch.tensor(anc, dtype=torch.int32))
+    got = _host(rows[:, :, :hq * d]).reshape(1, mq, hq, d).transpose(0, 2, 1, 3)
+    assert_rms_close(got, ref, 2e-2, "D=80 tree, strided out")
+    assert torch.all(rows[:, :, hq * d:] == 7.0)
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("hq,hk,q_len,L,causal", [(32, 8, 16, 2064, True), (64, 8, 16, 4112, True),
                                                  (8, 2, 5, 300, False), (16, 8, 12, 1000, True)])
@@ -229,17 +273,21 @@ def test_quantized_kv_32k(dev, bits):
     assert_rms_close(_host(out), ref, 2e-2, f"quantized {bits}-bit at 32k")
 
 
-def test_quantized_kv_fp16(dev):
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("L", [2000, 32768 + 16])
+def test_quantized_kv_fp16(dev, bits, L):
+    """fp16 caches at 8 and 4 bits, up to the 32k verify shape: as accurate as the plain kernel
+    over the dequantized cache (4-bit fields are unpacked exactly, no offset to cancel)."""
     from dspark_rocm import ops
 
-    kq, vq = _quant_cache(77, 1, 8, 2000, 128, 8, "f16", slack=8)
-    q = _mk(78, 1, 32, 8, 16, 1, 128, dt="f16")[0]
+    kq, vq = _quant_cache(77 + bits, 1, 8, L, 128, bits, "f16", slack=8)
+    q = _mk(78 + bits, 1, 32, 8, 16, 1, 128, dt="f16")[0]
     qd = _dev(q, "f16", dev)
-    out = ops.verify_attention_quantized(qd, kq, vq, scale=128 ** -0.5, causal=True, bits=8)
+    out = ops.verify_attention_quantized(qd, kq, vq, scale=128 ** -0.5, causal=True, bits=bits)
     assert out.dtype == torch.float16
-    ref = attn_ref.attention_quantized(q, _host_trip(kq), _host_trip(vq), 128 ** -0.5, 8, causal=True)
-    assert_rms_close(_host(out), ref, 2e-2, "quantized fp16")
-    plain = ops.verify_attention(qd, _dequant_on_device(kq, 8, "f16"), _dequant_on_device(vq, 8, "f16"),
+    ref = attn_ref.attention_quantized(q, _host_trip(kq), _host_trip(vq), 128 ** -0.5, bits, causal=True)
+    assert_rms_close(_host(out), ref, 2e-2, f"quantized fp16 {bits}-bit L{L}")
+    plain = ops.verify_attention(qd, _dequant_on_device(kq, bits, "f16"), _dequant_on_device(vq, bits, "f16"),
                                  scale=128 ** -0.5, causal=True)
     assert np.abs(_host(out) - ref).max() <= 1.05 * np.abs(_host(plain) - ref).max() + 1e-6
 
@@ -279,10 +327,11 @@ def test_quantized_cache_rollback_and_scope(dev):
 def test_refusals(dev):
     from dspark_rocm import _lib, ops
 
-    q = torch.zeros((1, 8, 4, 96), dtype=torch.bfloat16, device=dev)
-    k = torch.zeros((1, 2, 64, 96), dtype=torch.bfloat16, device=dev)
-    with pytest.raises(_lib.DsparkError):
-        ops.verify_attention(q, k, k, scale=0.1)                     # head_dim 96
+    for d in (100, 264):                                             # head_dim % 8 != 0, > 256
+        q = torch.zeros((1, 8, 4, d), dtype=torch.bfloat16, device=dev)
+        k = torch.zeros((1, 2, 64, d), dtype=torch.bfloat16, device=dev)
+        with pytest.raises((_lib.DsparkError, ValueError)):
+            ops.verify_attention(q, k, k, scale=0.1)
     q = torch.zeros((1, 8, 4, 64), dtype=torch.float16, device=dev)
     k = torch.zeros((1, 2, 64, 64), dtype=torch.bfloat16, device=dev)
     with pytest.raises(TypeError):

@@ -107,6 +107,44 @@ def test_multi_matches_separate_calls(dev, bits):
         assert torch.equal(multi[i], single), i
 
 
+C2_SHAPES = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288)]   # [N, K] of the 8B-shaped layer set
+
+
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
+@pytest.mark.parametrize("n,k", C2_SHAPES)
+def test_c2_layer_set_shapes_against_c_oracle(dev, n, k, m):
+    """Every distinct [N, K] of the 8-bit layer set (q/o, k/v, gate/up, down) at each verify
+    width, against the C restatement: the whole-K launch ([4096, 4096]) and the split-K plans."""
+    x, w, s, b = _problem(n + k + m, m, k, n, 8, quantized=True)
+    got = _run(dev, x, w, s, b, 8)
+    ref = c_oracle.qmm(quant_ref.bf16_bits(x), w, quant_ref.bf16_bits(s), quant_ref.bf16_bits(b), 8)
+    _check(got, ref.astype(np.float64), f"8-bit {n}x{k} M={m}")
+
+
+def test_multi_with_outlier_x_within_tolerance(dev):
+    """x whose groups of 64 span many binades (values near 1e3 and 1e-3 in one group): an 8-bit
+    [4096, 4096] matrix launched alone (whole-K) and inside a q/k/v launch (split-K) may differ
+    by an fp32 rounding of the bias term; both stay within 2 ulps of the exact result."""
+    from dspark_rocm import ops
+
+    r = rng(17)
+    x = randn_bf16(r, 16, 4096)
+    x[:, ::64] *= 1e3
+    x[:, 1::64] *= 1e-3
+    x = quant_ref.bf16_round(x)
+    mats = [quant_ref.random_packed(r, n, 4096, 8) for n in (4096, 1024, 1024)]
+    xd = to_dev_bf16(x, dev)
+    wd = [to_dev_packed(w, dev) for w, _, _ in mats]
+    sd = [to_dev_bf16(s, dev) for _, s, _ in mats]
+    bd = [to_dev_bf16(b, dev) for _, _, b in mats]
+    multi = ops.quantized_matmul_multi([xd], wd, sd, bd, bits=8)
+    for i, (w, s, b) in enumerate(mats):
+        single = ops.quantized_matmul(xd, wd[i], sd[i], bd[i], bits=8)
+        ref = qmm_ref.qmm_f64(x, w, s, b, 8)
+        _check(from_dev_bf16(single), ref, f"alone {i}")
+        _check(from_dev_bf16(multi[i]), ref, f"in the multi launch {i}")
+
+
 def test_strided_x_rows(dev):
     """x with a row stride larger than K (a view into a wider buffer)."""
     import torch
@@ -175,7 +213,11 @@ def test_workspace_reset_restores_counters(dev):
 
     from dspark_rocm import ops
 
-    x, w, s, b = _problem(61, 16, 4096, 4096, 8)
+    from dspark_rocm import _lib
+
+    # a split-K shape (8-bit 6144 x 4096: K slices, arrival counters and partials in the workspace)
+    assert _lib.load().dspark_qmm_affine_workspace(16, 4096, 6144, 8, 64) > 0
+    x, w, s, b = _problem(61, 16, 6144, 4096, 8)
     xd, wd, sd, bd = to_dev_bf16(x, dev), to_dev_packed(w, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
     want = ops.quantized_matmul(xd, wd, sd, bd, bits=8)
     ws = ops.new_qmm_workspace(dev, 8 << 20)

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 from _model_util import tiny_model, to_ref
-from _util import assert_rms_close
+from _util import ROPE_KAT_TOL, assert_rms_close, rope_kat_errors
 from oracle import model_ref, moe_ref, verify_ref
 
 pytestmark = pytest.mark.gpu
@@ -47,7 +47,7 @@ def test_rmsnorm_kernel(dev, H):
     assert np.abs(_np(y2) - model_ref.rmsnorm(h_ref, _np(w), 1e-6)).max() <= 2 ** -7 * np.abs(h_ref).max()
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128, 256])
 @pytest.mark.parametrize("Hq,Hk", [(8, 2), (5, 1)])   # 5 + 2 heads: a partly filled workgroup
 def test_qk_norm_rope_kv_kernel(dev, D, Hq, Hk):
     from dspark_rocm import ops
@@ -73,6 +73,32 @@ def test_qk_norm_rope_kv_kernel(dev, D, Hq, Hk):
     assert np.abs(_np(kc[:, pos0:pos0 + M]) - kr).max() <= tol
     assert np.array_equal(_np(vc[:, pos0:pos0 + M]), _np(v).reshape(M, Hk, D).transpose(1, 0, 2))
     assert not kc[:, :pos0].any() and not kc[:, pos0 + M:].any()   # nothing outside the block
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("base", [1e4, 1e6])
+def test_rope_kernel_frequency_schedule(dev, D, base):
+    """The closed-form RoPE KAT (tests/_util.rope_kat_errors) through the kernel. With unit q/k
+    norm weights and eps 0, RMSNorm maps e_i to r0 * e_i, r0 = bf16(sqrt(D)); dividing r0 out
+    leaves the rotation of e_i at position p, for the q output and the cached k alike."""
+    from dspark_rocm import ops
+
+    ones = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    r0 = float(model_ref.bf(np.float32(np.sqrt(D))))
+
+    def rope_fn(x, pos, b):
+        p = int(pos[0])
+        xv = torch.from_numpy(np.ascontiguousarray(x.reshape(1, D))).to(dev).to(torch.bfloat16)
+        kc = torch.zeros((1, p + 1, D), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        qo = torch.empty((1, 1, D), dtype=torch.bfloat16, device=dev)
+        ops.qk_norm_rope_kv(xv, xv, xv, ones, ones, heads=1, kv_heads=1, head_dim=D, eps=0.0, rope_base=b, pos0=p,
+                            q_out=qo, k_cache=kc, v_cache=vc)
+        q, k = _np(qo).reshape(D), _np(kc[0, p])
+        assert np.array_equal(q, k)
+        return q / r0
+
+    assert rope_kat_errors(rope_fn, D, base) <= ROPE_KAT_TOL
 
 
 def _argmax_ref(rows: np.ndarray) -> list[int]:
@@ -236,7 +262,7 @@ def test_speculative_trace_is_lossless_with_expected_accept_length(dev):
         truth = greedy[len(out):len(out) + cap]
         draft = [t if r.random() > 0.3 else (t + 1) % 512 for t in truth]
         n_expect = next((j for j, (d, t) in enumerate(zip(draft, truth)) if d != t), len(draft))
-        n, committed = tgt.greedy_round(out[-1], draft, cache)
+        n, committed, _ = tgt.greedy_round(out[-1], draft, cache)
         assert n == n_expect, (rounds, draft, truth)
         out += committed
         expected_acc.append(n + 1)
@@ -245,6 +271,99 @@ def test_speculative_trace_is_lossless_with_expected_accept_length(dev):
     assert out[:steps] == greedy[:steps]
     # the first token came from the prompt's forward; the rounds committed the rest
     assert verify_ref.mean_accept_len(sum(expected_acc), rounds) == (len(out) - 1) / rounds
+
+
+def test_verify_tap_returns_the_tapped_hidden_states(dev):
+    """Target.verify(ids, cache, tap) -> (logits, fused [1, M, n_tap * H]): the residual stream
+    after each tapped layer in layer order, whatever the order, duplicates or out-of-range
+    entries of ``tap`` (target.py:208-220, :642-677). The tap changes no logit bit; each column
+    block is bitwise the block a one-layer tap returns; against the oracle's tapped forward and
+    the module path's capture within 2e-2 x RMS per block; ``tap=None`` returns None; the
+    prefill chunk returns the same capture through the module path (target.py:435-465)."""
+    from dspark_rocm.model import Target, tap_layers
+
+    model = tiny_model(dev, seed=13, num_hidden_layers=4)
+    H = model.args.hidden_size
+    tgt = Target(model)
+    tap = [3, 1, 1, 9, -2]
+    assert tap_layers(tap, 4) == (1, 3)
+    r = np.random.Generator(np.random.PCG64(14))
+    prefix = r.integers(0, 512, 20).tolist()
+    block = r.integers(0, 512, 12).tolist()
+    runs = {}
+    for key, t in (("none", None), ("both", tap), ("l1", [1]), ("l3", [3])):
+        cache = tgt.make_cache(64)
+        tgt.verify(torch.tensor([prefix[:16]]), cache)
+        tgt.verify(torch.tensor([prefix[16:]]), cache)
+        logits, fused = tgt.verify(torch.tensor([block]), cache, t)
+        runs[key] = (logits.clone(), None if fused is None else fused.clone())
+    assert runs["none"][1] is None
+    fused = runs["both"][1]
+    assert fused.shape == (1, 12, 2 * H) and fused.dtype == torch.bfloat16
+    for key in ("both", "l1", "l3"):
+        assert torch.equal(runs[key][0], runs["none"][0]), key
+    assert torch.equal(fused[..., :H], runs["l1"][1]) and torch.equal(fused[..., H:], runs["l3"][1])
+
+    ref = to_ref(model)
+    ref.forward(prefix)
+    ref.forward(block, tap=tap)
+    want = ref.fused
+    assert want.shape == (12, 2 * H)
+    for j in range(2):
+        assert_rms_close(_np(fused[0, :, j * H:(j + 1) * H]), want[:, j * H:(j + 1) * H], 2e-2, f"tap block {j}")
+    # the module path (Target.run) and a prefill chunk capture the same stream
+    cm = tgt.make_cache(64)
+    tgt.prefill(torch.tensor([prefix]), cm)
+    with torch.no_grad():
+        logits_m, fused_m = tgt.run(torch.tensor([block]), cm, tap)
+    assert fused_m.shape == fused.shape
+    assert_rms_close(_np(fused_m[0]), _np(fused[0]), 2e-2, "module path capture")
+    cp = tgt.make_cache(64)
+    with torch.no_grad():
+        none, fused_p = tgt.prefill(torch.tensor([prefix + block]), cp, tap)
+        lp, nofused = tgt.prefill(torch.tensor([block[:3]]), cp, want_logits=True)
+    assert none is None and nofused is None and lp.shape == (1, 1, model.args.vocab_size)
+    assert fused_p.shape == (1, 32, 2 * H)
+    assert_rms_close(_np(fused_p[0, 20:]), want, 2e-2, "prefill capture")
+
+
+def test_speculative_trace_feeds_the_drafter_its_context_rows(dev):
+    """The DSpark loop's context update (generate.py:1547, :1590-1593): every round hands
+    fused[:, :n + 1] (the tapped states of [pending, accepted drafts]) to the drafter. A stub
+    update_context checks each call's shape and offset; over the whole trace the rows it
+    received are the oracle's tapped stream over the committed tokens, position for position."""
+    from dspark_rocm.model import Target
+
+    model = tiny_model(dev, seed=15, num_hidden_layers=3)
+    H = model.args.hidden_size
+    tgt = Target(model)
+    tap = [0, 2]
+    r = np.random.Generator(np.random.PCG64(16))
+    prompt = r.integers(0, 512, 9).tolist()
+    cache = tgt.make_cache(128)
+    logits, _ = tgt.verify(torch.tensor([prompt]), cache, tap)
+    out = [int(torch.argmax(logits[0, -1].float()))]
+    received = []
+
+    def update_context(rows, ctx_offset):
+        assert rows.shape[0] == 1 and rows.shape[2] == len(tap) * H
+        assert ctx_offset == len(prompt) + sum(x.shape[1] for x in received)
+        received.append(rows.clone())
+
+    n_cached = len(prompt)
+    while len(out) < 40:
+        draft = [int(t) for t in r.integers(0, 512, int(r.integers(0, 6)))]
+        n, committed, ctx = tgt.greedy_round(out[-1], draft, cache, tap)
+        assert ctx.shape == (1, n + 1, len(tap) * H)
+        update_context(ctx, n_cached)
+        n_cached += n + 1
+        out += committed
+    got = torch.cat(received, dim=1)[0]
+    ref = to_ref(model)
+    ref.forward(prompt + out[:-1], tap=tap)
+    want = ref.fused[len(prompt):]
+    assert got.shape == want.shape
+    assert_rms_close(_np(got), want, 2e-2, "context rows over the trace")
 
 
 def test_packed_engine_is_bitwise_the_reference_layout_engine(dev):

@@ -137,12 +137,12 @@ def test_half_gemm_variant_within_the_qmm_bar(dev, bits):
 
 
 def test_prefill_fills_caches_identically_with_the_wide_path(dev, monkeypatch):
-    """Target.prefill with the wide path forced on (every shape verified at 256 rows) leaves
+    """prefill_plain (Target.prefill per chunk) with the wide path forced on (every shape verified at 256 rows) leaves
     bit-identical caches and logits to the stock prefill, over two chunks (300 + 300 rows)."""
     from _model_util import tiny_model
 
     from dspark_rocm import calibrate, wide_gemm
-    from dspark_rocm.model import Target
+    from dspark_rocm.model import Target, prefill_plain
 
     model = tiny_model(dev, seed=21, hidden_size=512, intermediate_size=1536)
     tgt = Target(model)
@@ -152,7 +152,7 @@ def test_prefill_fills_caches_identically_with_the_wide_path(dev, monkeypatch):
     monkeypatch.setattr(calibrate, "WIDE_GEMM_SHAPES", None)
     stock_cache = tgt.make_cache(640)
     with torch.no_grad():
-        stock = tgt.prefill(ids, stock_cache, chunk=300)
+        stock, _ = prefill_plain(tgt, ids, stock_cache, chunk=300)
     assert calibrate.apply_wide_gemm(model, target_repo="synthetic", min_rows=256, verbose=False) == 256
     assert len(calibrate.WIDE_GEMM_SHAPES) == len({wide_gemm.shape_key(m) for m in wide_gemm.quantized_linears(model)})
     n = []
@@ -160,7 +160,7 @@ def test_prefill_fills_caches_identically_with_the_wide_path(dev, monkeypatch):
     monkeypatch.setattr(wide_gemm, "wide_rows", lambda *a, **k: n.append(1) or real(*a, **k))
     wide_cache = tgt.make_cache(640)
     with torch.no_grad():
-        wide = tgt.prefill(ids, wide_cache, chunk=300)
+        wide, _ = prefill_plain(tgt, ids, wide_cache, chunk=300)
     assert n, "no projection took the wide path"
     assert stock.shape == (1, 1, model.args.vocab_size) and torch.equal(wide, stock)
     for a, b in zip(stock_cache, wide_cache):

@@ -131,7 +131,11 @@ def test_multirow_plan_kats():
     with pytest.raises(_lib.DsparkError):
         plan(64, 2, 16, 128, 32768)                  # gqa * q_len = 512 rows > 256
     with pytest.raises(_lib.DsparkError):
-        plan(32, 8, 16, 96, 4096)                    # head_dim 96 unsupported
+        plan(32, 8, 16, 100, 4096)                   # head_dim % 8 != 0
+    with pytest.raises(_lib.DsparkError):
+        plan(32, 8, 16, 264, 4096)                   # head_dim > 256
+    assert plan(32, 8, 16, 96, 4096) == plan(32, 8, 16, 128, 4096)   # runs on the 128 instance
+    assert plan(24, 4, 16, 192, 4096) == plan(24, 4, 16, 256, 4096)
 
 
 CFG = None

@@ -5,9 +5,11 @@ weights on the CPU (two independent implementations of mlx-lm's decoder semantic
 from __future__ import annotations
 
 import numpy as np
+import pytest
 import torch
 
 from _model_util import tiny_model, to_ref
+from _util import ROPE_KAT_TOL, rope_kat_errors
 from oracle import model_ref, quant_ref
 
 
@@ -35,6 +37,42 @@ def test_rope_invariants():
     dots = [float(np.sum(model_ref.rope(q, [p + 7], 1e4).astype(np.float64) *
                          model_ref.rope(k, [p], 1e4).astype(np.float64))) for p in (0, 33, 500)]
     assert max(dots) - min(dots) < 0.05 * np.abs(q).sum()                         # relative position only
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("base", [1e4, 1e6])
+def test_rope_frequency_schedule_closed_form(D, base):
+    assert rope_kat_errors(model_ref.rope, D, base) <= ROPE_KAT_TOL
+
+
+def test_rope_kat_rejects_wrong_schedules():
+    """The KAT fails a plausible slip: the exponent -i/D instead of -2i/D, or the wrong base."""
+    def wrong_exponent(x, pos, base):
+        x = np.asarray(x, np.float32)
+        D = x.shape[-1]
+        half = D // 2
+        inv = base ** (-np.arange(half) / D)
+        ang = np.asarray(pos, np.float64)[:, None] * inv[None, :]
+        c, s = np.cos(ang), np.sin(ang)
+        x1, x2 = x[..., :half].astype(np.float64), x[..., half:].astype(np.float64)
+        return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+
+    def wrong_base(x, pos, base):
+        return model_ref.rope(x, pos, base * 10)
+
+    def traditional_pairs(x, pos, base):   # pairs (2i, 2i+1) instead of (i, i + D/2)
+        x = np.asarray(x, np.float64)
+        D = x.shape[-1]
+        inv = base ** (-2.0 * np.arange(D // 2) / D)
+        ang = np.asarray(pos, np.float64)[:, None] * inv[None, :]
+        c, s = np.cos(ang), np.sin(ang)
+        y = x.copy()
+        y[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
+        y[..., 1::2] = x[..., 0::2] * s + x[..., 1::2] * c
+        return y
+
+    for fn in (wrong_exponent, wrong_base, traditional_pairs):
+        assert rope_kat_errors(fn, 128, 1e6) > 10 * ROPE_KAT_TOL, fn.__name__
 
 
 def test_numpy_forward_matches_torch_module_path_on_cpu():
