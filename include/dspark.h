@@ -449,6 +449,27 @@ int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k, int64_t ld
                            void* k_cache, const int64_t k_cache_strides[2], void* v_cache,
                            const int64_t v_cache_strides[2], dspark_stream stream);
 
+/* dspark_qk_norm_rope_kv for a quantized KV cache (mlx-lm QuantizedKVCache, which the
+ * reference's dense targets build for every layer when kv_bits is set, target.py:166-184): the
+ * same q output, and the rotated k row and the v row (each as the bf16 values the plain entry
+ * point would write) quantized into the cache row at position pos0 + m: `bits`-bit fields
+ * along D (low bits first) in k_words / v_words [Hk, capacity, D*bits/32] (strides (head,
+ * position) in words), one bf16 scale and bias per 64 values in k_scales / k_biases and
+ * v_scales / v_biases [Hk, capacity, D/64] (strides (head, position) in elements). Per group:
+ * scale = bf16((max - min) / (2^bits - 1)), bias = bf16(min), field = round-half-even((x - bias)
+ * / scale) clamped to the range (scale 0 divides by 1), each step one fp32 operation: the rule
+ * of this build's quantizer (dspark_rocm.quant.quantize_rows; mx.quantize's own choice is not
+ * reproducible without MLX). Replaces QuantizedKVCache.update_and_fetch's mx.quantize of the
+ * new rows. D in {64, 128, 256}, bits 4 or 8, group_size 64. */
+int dspark_qk_norm_rope_kv_quantized(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                                     int64_t ldv, int64_t M, int64_t Hq, int64_t Hk, int64_t D,
+                                     const void* q_norm_w, const void* k_norm_w, float eps, float rope_base,
+                                     int64_t pos0, void* q_out, uint32_t* k_words, void* k_scales,
+                                     void* k_biases, const int64_t k_strides[2], const int64_t k_scale_strides[2],
+                                     uint32_t* v_words, void* v_scales, void* v_biases, const int64_t v_strides[2],
+                                     const int64_t v_scale_strides[2], int bits, int group_size,
+                                     dspark_stream stream);
+
 /* h = bf16(bf16(g * bf16(sigmoid(g))) * u) over [M, N] (N % 8 == 0): MLP's silu(gate) * up. */
 int dspark_swiglu(const void* g, int64_t ldg, const void* u, int64_t ldu, int64_t M, int64_t N, void* h,
                   int64_t ldh, dspark_stream stream);

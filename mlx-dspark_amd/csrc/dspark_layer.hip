@@ -156,10 +156,168 @@ struct QkArgs {
   u16* kc;
   u16* vc;
   long ldq, ldk, ldv;
-  long kch, kcs, vch, vcs;  // cache strides (head, position) in elements
+  long kch, kcs, vch, vcs;  // cache strides (head, position) in elements (words when quantized)
   int M, Hq, Hk, pos0, D;
   float eps, log2_base;
+  // quantized cache (mlx-lm QuantizedKVCache): scales and biases of K and V, strides (head,
+  // position) in elements; the words are kc / vc
+  u16* ks;
+  u16* kb;
+  u16* vs;
+  u16* vb;
+  long ksh, kss, vsh, vss;
 };
+
+// RMSNorm-scaled pair (x1, x2) = elements (i, i + D/2) of a head, rotated by RoPE at `pos`:
+// the two results before their bf16 rounding (shared by the plain and quantized cache writes, so
+// both round the same values)
+__device__ __forceinline__ void norm_rope_pair(float x1, float x2, float w1, float w2, float inv, int i, int D,
+                                               int pos, float log2_base, float& r1, float& r2) {
+  const float n1 = bf16r(bf16r(x1 * inv) * w1);
+  const float n2 = bf16r(bf16r(x2 * inv) * w2);
+  const float inv_freq = exp2f(-(2.0f * (float)i / (float)D) * log2_base);
+  const float ang = (float)pos * inv_freq;
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  r1 = n1 * cs - n2 * sn;
+  r2 = n1 * sn + n2 * cs;
+}
+
+// One cache row (a head's D values, held as in qk_norm_rope_kv_kernel: lane l has d = l + 64 j
+// in a[j] and d + D/2 in b[j]) quantized in groups of 64 with the rule of the build's quantizer
+// (dspark_rocm.quant.quantize_rows): scale = bf16((max - min) / (2^QB - 1)), bias = bf16(min),
+// q = clamp(round_half_even((x - bias) / scale), 0, 2^QB - 1) (scale 0 divides by 1), each an
+// fp32 operation rounded to nearest. Fields are stored as bytes of the row's words (field j at
+// bits QB*(j % (32/QB)) of word j / (32/QB), low bits first = byte-addressed little-endian).
+template <int NP, int QB>
+__device__ __forceinline__ void store_quant_row(const float (&a)[NP], const float (&b)[NP], int lane, int D,
+                                                unsigned char* wrow, u16* srow, u16* brow) {
+  const int HALF = D >> 1, G = D >> 6;
+  constexpr float kLevels = (float)((1 << QB) - 1);
+  float scale[4], bias[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int d = lane + 64 * j;
+      if (d < HALF) {
+        if ((d >> 6) == g) {
+          lo = fminf(lo, a[j]);
+          hi = fmaxf(hi, a[j]);
+        }
+        if (((d + HALF) >> 6) == g) {
+          lo = fminf(lo, b[j]);
+          hi = fmaxf(hi, b[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      lo = fminf(lo, shfl_xor(lo, o));
+      hi = fmaxf(hi, shfl_xor(hi, o));
+    }
+    const u16 sbits = f2bf(__fdiv_rn(__fsub_rn(hi, lo), kLevels)), bbits = f2bf(lo);
+    if (g < G && lane == 0) {
+      srow[g] = sbits;
+      brow[g] = bbits;
+    }
+    const float s32 = bf2f(sbits);
+    scale[g] = s32 == 0.f ? 1.f : s32;
+    bias[g] = bf2f(bbits);
+  }
+  auto field = [&](float x, int d) {
+    const int g = d >> 6;
+    const float q = rintf(__fdiv_rn(__fsub_rn(x, bias[g]), scale[g]));
+    return (u32)fminf(fmaxf(q, 0.f), kLevels);
+  };
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int d = lane + 64 * j;
+    const bool on = d < HALF;
+    const u32 qa = on ? field(a[j], d) : 0u, qb = on ? field(b[j], d + HALF) : 0u;
+    if constexpr (QB == 8) {
+      if (on) {
+        wrow[d] = (unsigned char)qa;
+        wrow[d + HALF] = (unsigned char)qb;
+      }
+    } else {
+      // two fields per byte: the even lane takes its odd neighbour's (d + 1 sits in lane + 1)
+      const u32 na = (u32)__builtin_amdgcn_ds_bpermute((lane ^ 1) << 2, (int)qa);
+      const u32 nb = (u32)__builtin_amdgcn_ds_bpermute((lane ^ 1) << 2, (int)qb);
+      if (on && !(lane & 1)) {
+        wrow[d >> 1] = (unsigned char)(qa | (na << 4));
+        wrow[(d + HALF) >> 1] = (unsigned char)(qb | (nb << 4));
+      }
+    }
+  }
+}
+
+// qk_norm_rope_kv_kernel writing a quantized cache: the same q output and the same rotated k
+// (rounded to bf16) and v values, quantized into the cache rows (store_quant_row)
+template <int NP, int QB>
+__global__ __launch_bounds__(64) void qk_norm_rope_qkv_kernel(const QkArgs a) {
+  const int D = a.D, HALF = a.D >> 1;
+  const int m = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
+  const int pos = a.pos0 + m;
+  float o1[NP], o2[NP];
+  if (hh >= a.Hq + a.Hk) {  // V head
+    const int h = hh - a.Hq - a.Hk;
+    const u16* src = a.v + (long)m * a.ldv + (long)h * D;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int i = lane + 64 * j;
+      o1[j] = i < HALF ? bf2f(src[i]) : 0.f;
+      o2[j] = i < HALF ? bf2f(src[i + HALF]) : 0.f;
+    }
+    store_quant_row<NP, QB>(o1, o2, lane, D,
+                            reinterpret_cast<unsigned char*>(a.vc + 2 * ((long)h * a.vch + (long)pos * a.vcs)),
+                            a.vs + (long)h * a.vsh + (long)pos * a.vss, a.vb + (long)h * a.vsh + (long)pos * a.vss);
+    return;
+  }
+  const bool isq = hh < a.Hq;
+  const int h = isq ? hh : hh - a.Hq;
+  const u16* src = isq ? a.q + (long)m * a.ldq + (long)h * D : a.k + (long)m * a.ldk + (long)h * D;
+  const u16* w = isq ? a.qw : a.kw;
+  float x1[NP], x2[NP];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int i = lane + 64 * j;
+    const bool on = i < HALF;
+    x1[j] = on ? bf2f(src[i]) : 0.f;
+    x2[j] = on ? bf2f(src[i + HALF]) : 0.f;
+    ss += x1[j] * x1[j] + x2[j] * x2[j];
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int i = lane + 64 * j;
+    o1[j] = o2[j] = 0.f;
+    if (i < HALF) {
+      float r1, r2;
+      norm_rope_pair(x1[j], x2[j], bf2f(w[i]), bf2f(w[i + HALF]), inv, i, D, pos, a.log2_base, r1, r2);
+      o1[j] = bf16r(r1);
+      o2[j] = bf16r(r2);
+    }
+  }
+  if (isq) {
+    u16* dst = a.qout + ((long)h * a.M + m) * D;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int i = lane + 64 * j;
+      if (i < HALF) {
+        dst[i] = f2bf(o1[j]);
+        dst[i + HALF] = f2bf(o2[j]);
+      }
+    }
+    return;
+  }
+  store_quant_row<NP, QB>(o1, o2, lane, D,
+                          reinterpret_cast<unsigned char*>(a.kc + 2 * ((long)h * a.kch + (long)pos * a.kcs)),
+                          a.ks + (long)h * a.ksh + (long)pos * a.kss, a.kb + (long)h * a.ksh + (long)pos * a.kss);
+}
 
 // one wave per (row, head); lane l owns the RoPE pairs (i, i + D/2) for i = l + 64 j, j < NP
 // (NP = ceil(D / 128): head dims up to 128 take one pair per lane, up to 256 two)
@@ -202,14 +360,10 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kv_kernel(const QkArgs a) {
   for (int j = 0; j < NP; ++j) {
     const int i = lane + 64 * j;
     if (i >= HALF) break;
-    const float n1 = bf16r(bf16r(x1[j] * inv) * bf2f(w[i]));
-    const float n2 = bf16r(bf16r(x2[j] * inv) * bf2f(w[i + HALF]));
-    const float inv_freq = exp2f(-(2.0f * (float)i / (float)D) * a.log2_base);
-    const float ang = (float)(a.pos0 + m) * inv_freq;
-    float sn, cs;
-    sincosf(ang, &sn, &cs);
-    dst[i] = f2bf(n1 * cs - n2 * sn);
-    dst[i + HALF] = f2bf(n1 * sn + n2 * cs);
+    float r1, r2;
+    norm_rope_pair(x1[j], x2[j], bf2f(w[i]), bf2f(w[i + HALF]), inv, i, D, a.pos0 + m, a.log2_base, r1, r2);
+    dst[i] = f2bf(r1);
+    dst[i + HALF] = f2bf(r2);
   }
 }
 
@@ -434,21 +588,23 @@ extern "C" int dspark_rmsnorm(const void* x, int64_t ldx, const void* r, int64_t
   return check_launch("rmsnorm");
 }
 
-extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
-                                      int64_t ldv, int64_t M, int64_t Hq, int64_t Hk, int64_t D, const void* q_norm_w,
-                                      const void* k_norm_w, float eps, float rope_base, int64_t pos0, void* q_out,
-                                      void* k_cache, const int64_t k_cache_strides[2], void* v_cache,
-                                      const int64_t v_cache_strides[2], dspark_stream stream) {
-  if (!q || !k || !v || !q_norm_w || !k_norm_w || !q_out || !k_cache || !v_cache || !k_cache_strides || !v_cache_strides)
-    return fail(DSPARK_ERR_ARG, "qk_norm_rope_kv: null pointer");
+namespace dspark {
+namespace {
+// The checks and arguments shared by the plain and quantized cache writes.
+int qk_args(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t M, int64_t Hq,
+            int64_t Hk, int64_t D, const void* q_norm_w, const void* k_norm_w, float eps, float rope_base,
+            int64_t pos0, void* q_out, void* k_cache, const int64_t* k_strides, void* v_cache,
+            const int64_t* v_strides, const char* what, QkArgs& a) {
+  if (!q || !k || !v || !q_norm_w || !k_norm_w || !q_out || !k_cache || !v_cache || !k_strides || !v_strides)
+    return fail(DSPARK_ERR_ARG, "%s: null pointer", what);
   if (D < 8 || D > 256 || D % 8)
-    return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: head_dim %lld (a multiple of 8 up to 256)", (long long)D);
+    return fail(DSPARK_ERR_SHAPE, "%s: head_dim %lld (a multiple of 8 up to 256)", what, (long long)D);
   if (M < 1 || M > 65535 || Hq < 1 || Hk < 1 || Hq + 2 * Hk > 65535 || pos0 < 0 || pos0 + M > (1L << 30))
-    return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: M=%lld Hq=%lld Hk=%lld pos0=%lld", (long long)M, (long long)Hq,
+    return fail(DSPARK_ERR_SHAPE, "%s: M=%lld Hq=%lld Hk=%lld pos0=%lld", what, (long long)M, (long long)Hq,
                 (long long)Hk, (long long)pos0);
   if (ldq < Hq * D || ldk < Hk * D || ldv < Hk * D || !(rope_base > 0.f))
-    return fail(DSPARK_ERR_SHAPE, "qk_norm_rope_kv: row strides below the head widths or rope_base <= 0");
-  QkArgs a{};
+    return fail(DSPARK_ERR_SHAPE, "%s: row strides below the head widths or rope_base <= 0", what);
+  a = QkArgs{};
   a.q = static_cast<const u16*>(q);
   a.k = static_cast<const u16*>(k);
   a.v = static_cast<const u16*>(v);
@@ -460,10 +616,10 @@ extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k,
   a.ldq = ldq;
   a.ldk = ldk;
   a.ldv = ldv;
-  a.kch = k_cache_strides[0];
-  a.kcs = k_cache_strides[1];
-  a.vch = v_cache_strides[0];
-  a.vcs = v_cache_strides[1];
+  a.kch = k_strides[0];
+  a.kcs = k_strides[1];
+  a.vch = v_strides[0];
+  a.vcs = v_strides[1];
   a.M = (int)M;
   a.Hq = (int)Hq;
   a.Hk = (int)Hk;
@@ -471,11 +627,61 @@ extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k,
   a.D = (int)D;
   a.eps = eps;
   a.log2_base = log2f(rope_base);
+  return DSPARK_OK;
+}
+}  // namespace
+}  // namespace dspark
+
+extern "C" int dspark_qk_norm_rope_kv(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                                      int64_t ldv, int64_t M, int64_t Hq, int64_t Hk, int64_t D, const void* q_norm_w,
+                                      const void* k_norm_w, float eps, float rope_base, int64_t pos0, void* q_out,
+                                      void* k_cache, const int64_t k_cache_strides[2], void* v_cache,
+                                      const int64_t v_cache_strides[2], dspark_stream stream) {
+  QkArgs a;
+  const int st = qk_args(q, ldq, k, ldk, v, ldv, M, Hq, Hk, D, q_norm_w, k_norm_w, eps, rope_base, pos0, q_out,
+                         k_cache, k_cache_strides, v_cache, v_cache_strides, "qk_norm_rope_kv", a);
+  if (st) return st;
   const dim3 grid((unsigned)M, (unsigned)(Hq + 2 * Hk));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D <= 128) hipLaunchKernelGGL(qk_norm_rope_kv_kernel<1>, grid, dim3(64), 0, s, a);
   else hipLaunchKernelGGL(qk_norm_rope_kv_kernel<2>, grid, dim3(64), 0, s, a);
   return check_launch("qk_norm_rope_kv");
+}
+
+extern "C" int dspark_qk_norm_rope_kv_quantized(
+    const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, int64_t M, int64_t Hq,
+    int64_t Hk, int64_t D, const void* q_norm_w, const void* k_norm_w, float eps, float rope_base, int64_t pos0,
+    void* q_out, uint32_t* k_words, void* k_scales, void* k_biases, const int64_t k_strides[2],
+    const int64_t k_scale_strides[2], uint32_t* v_words, void* v_scales, void* v_biases, const int64_t v_strides[2],
+    const int64_t v_scale_strides[2], int bits, int group_size, dspark_stream stream) {
+  const char* what = "qk_norm_rope_kv_quantized";
+  QkArgs a;
+  int st = qk_args(q, ldq, k, ldk, v, ldv, M, Hq, Hk, D, q_norm_w, k_norm_w, eps, rope_base, pos0, q_out, k_words,
+                   k_strides, v_words, v_strides, what, a);
+  if (st) return st;
+  if (bits != 4 && bits != 8) return fail(DSPARK_ERR_UNSUPPORTED, "%s: bits=%d (4 or 8)", what, bits);
+  if (group_size != 64) return fail(DSPARK_ERR_UNSUPPORTED, "%s: group_size=%d (64)", what, group_size);
+  if (D != 64 && D != 128 && D != 256) return fail(DSPARK_ERR_SHAPE, "%s: head_dim %lld (64, 128 or 256)", what, (long long)D);
+  if (!k_scales || !k_biases || !v_scales || !v_biases || !k_scale_strides || !v_scale_strides)
+    return fail(DSPARK_ERR_ARG, "%s: null pointer", what);
+  a.ks = static_cast<u16*>(k_scales);
+  a.kb = static_cast<u16*>(k_biases);
+  a.vs = static_cast<u16*>(v_scales);
+  a.vb = static_cast<u16*>(v_biases);
+  a.ksh = k_scale_strides[0];
+  a.kss = k_scale_strides[1];
+  a.vsh = v_scale_strides[0];
+  a.vss = v_scale_strides[1];
+  const dim3 grid((unsigned)M, (unsigned)(Hq + 2 * Hk));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (bits == 8) {
+    if (D <= 128) hipLaunchKernelGGL((qk_norm_rope_qkv_kernel<1, 8>), grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL((qk_norm_rope_qkv_kernel<2, 8>), grid, dim3(64), 0, s, a);
+  } else {
+    if (D <= 128) hipLaunchKernelGGL((qk_norm_rope_qkv_kernel<1, 4>), grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL((qk_norm_rope_qkv_kernel<2, 4>), grid, dim3(64), 0, s, a);
+  }
+  return check_launch(what);
 }
 
 extern "C" int dspark_swiglu(const void* g, int64_t ldg, const void* u, int64_t ldu, int64_t M, int64_t N, void* h,

@@ -149,6 +149,11 @@ SIGNATURES: dict[str, tuple] = {
     "dspark_qk_norm_rope_kv": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64,
                                        c_void_p, c_void_p, c_float, c_float, c_i64, c_void_p, c_void_p, c_i64_p,
                                        c_void_p, c_i64_p, c_void_p]),
+    "dspark_qk_norm_rope_kv_quantized": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64,
+                                                 c_i64, c_i64, c_void_p, c_void_p, c_float, c_float, c_i64,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p, c_i64_p, c_i64_p,
+                                                 c_void_p, c_void_p, c_void_p, c_i64_p, c_i64_p, c_int, c_int,
+                                                 c_void_p]),
     "dspark_swiglu": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p]),
     "dspark_argmax_rows": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p]),
     "dspark_greedy_accept": (c_int, [c_void_p, c_i64, c_void_p, c_void_p, c_void_p]),

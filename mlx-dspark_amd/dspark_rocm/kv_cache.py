@@ -133,6 +133,17 @@ class QuantizedKVCache:
         self.offset += t
         return self.fetch()
 
+    def reserve(self, t: int) -> None:
+        """Make room for ``t`` more rows at ``offset`` (a kernel then writes them in place)."""
+        if self.offset + t > self.capacity:
+            self._grow(self.offset + t)
+
+    def advance(self, t: int) -> None:
+        """Commit ``t`` rows a kernel wrote at ``offset`` (after :meth:`reserve`)."""
+        if self.offset + t > self.capacity:
+            raise ValueError(f"advance({t}) past capacity {self.capacity} at offset {self.offset}")
+        self.offset += t
+
     def fetch(self):
         view = lambda trip: tuple(a[:, :, :self.offset] for a in trip)
         return view(self.keys), view(self.values)

@@ -34,7 +34,7 @@ from torch import nn
 
 from . import fast, ops
 from ._lib import load as _lib_load
-from .kv_cache import KVCache
+from .kv_cache import KVCache, QuantizedKVCache
 from .nn import QuantizedLinear
 
 
@@ -91,8 +91,15 @@ class Attention(nn.Module):
         q = rope(q, cache.offset, a.rope_theta)
         k = rope(k, cache.offset, a.rope_theta)
         keys, values = cache.update_and_fetch(k, v)
-        out = fast.scaled_dot_product_attention(q.contiguous(), keys, values, scale=d ** -0.5,
-                                                mask="causal" if L > 1 else None)
+        mask = "causal" if L > 1 else None
+        if hasattr(cache, "bits"):
+            # mlx-lm's attention helper dispatches per cache: a quantized cache takes
+            # quantized_scaled_dot_product_attention over its (words, scales, biases) triples
+            out = fast.quantized_scaled_dot_product_attention(q.contiguous(), keys, values, scale=d ** -0.5,
+                                                              mask=mask, group_size=cache.group_size,
+                                                              bits=cache.bits)
+        else:
+            out = fast.scaled_dot_product_attention(q.contiguous(), keys, values, scale=d ** -0.5, mask=mask)
         return self.o_proj(out.transpose(1, 2).reshape(B, L, hq * d))
 
 
@@ -152,9 +159,15 @@ class DenseModel(nn.Module):
         embed = torch.randn((args.vocab_size, H), generator=g, device=device).to(torch.bfloat16)
         return cls(args, embed, layers, normw(H), lin(args.vocab_size, H, args.lm_head_bits))
 
-    def make_cache(self, capacity: int = 0) -> list[KVCache]:
+    def make_cache(self, capacity: int = 0, kv_bits: int | None = None, kv_group_size: int = 64) -> list:
+        """One KV cache per layer; with ``kv_bits`` (4 or 8) every layer's cache is quantized
+        (target.py:166-184: a dense target replaces each plain cache by mlx-lm's
+        QuantizedKVCache)."""
         a = self.args
         dev = self.embed_tokens.device
+        if kv_bits:
+            return [QuantizedKVCache(1, a.num_key_value_heads, a.head_dim, bits=kv_bits, group_size=kv_group_size,
+                                     device=dev, capacity=capacity) for _ in range(a.num_hidden_layers)]
         return [KVCache(1, a.num_key_value_heads, a.head_dim, device=dev, capacity=capacity)
                 for _ in range(a.num_hidden_layers)]
 
@@ -320,13 +333,24 @@ class VerifyEngine:
                 ops.rmsnorm(hcur, layer.input_layernorm, eps, residual=r, h_out=dst, out=y)
                 hcur = dst
             self._qmm(y, [at.q_proj, at.k_proj, at.v_proj], [self.q[:M], self.k[:M], self.v[:M]])
-            ops.qk_norm_rope_kv(self.q[:M], self.k[:M], self.v[:M], at.q_norm, at.k_norm, heads=hq, kv_heads=hk,
-                                head_dim=d, eps=eps, rope_base=a.rope_theta, pos0=pos0, q_out=qatt[0],
-                                k_cache=c.keys[0], v_cache=c.values[0])
-            kv, vv = c.keys[:, :, :L], c.values[:, :, :L]
             att = self.att[:M]
-            ops.verify_attention_into(qatt, kv, vv, att, (M * hq * d, d, hq * d), scale=d ** -0.5, causal=M > 1,
-                                      workspace=self.attn_ws)
+            ostr = (M * hq * d, d, hq * d)
+            if hasattr(c, "bits"):      # quantized cache: rows quantized as written, attention on the triples
+                ops.qk_norm_rope_kv_quantized(self.q[:M], self.k[:M], self.v[:M], at.q_norm, at.k_norm, heads=hq,
+                                              kv_heads=hk, head_dim=d, eps=eps, rope_base=a.rope_theta, pos0=pos0,
+                                              q_out=qatt[0], k_cache=tuple(t[0] for t in c.keys),
+                                              v_cache=tuple(t[0] for t in c.values), bits=c.bits,
+                                              group_size=c.group_size)
+                ops.verify_attention_quantized(qatt, tuple(t[:, :, :L] for t in c.keys),
+                                               tuple(t[:, :, :L] for t in c.values), scale=d ** -0.5, causal=M > 1,
+                                               bits=c.bits, group_size=c.group_size, out=att, out_strides=ostr,
+                                               workspace=self.attn_ws)
+            else:
+                ops.qk_norm_rope_kv(self.q[:M], self.k[:M], self.v[:M], at.q_norm, at.k_norm, heads=hq,
+                                    kv_heads=hk, head_dim=d, eps=eps, rope_base=a.rope_theta, pos0=pos0,
+                                    q_out=qatt[0], k_cache=c.keys[0], v_cache=c.values[0])
+                ops.verify_attention_into(qatt, c.keys[:, :, :L], c.values[:, :, :L], att, ostr, scale=d ** -0.5,
+                                          causal=M > 1, workspace=self.attn_ws)
             self._qmm(att, [at.o_proj], [r])
             ops.rmsnorm(hcur, layer.post_attention_layernorm, eps, residual=r, h_out=h, out=y)
             hcur = h
@@ -350,13 +374,17 @@ class Target:
     """The reference's Target surface for a dense model: ``make_cache``, ``verify``,
     ``plain``, ``rollback`` (target.py:166-184, :642-696), plus the greedy round."""
 
-    def __init__(self, model: DenseModel, max_rows: int = 16, packed: bool = True):
+    def __init__(self, model: DenseModel, max_rows: int = 16, packed: bool = True, kv_bits: int | None = None,
+                 kv_group_size: int = 64):
         self.model = model
         self.engine = VerifyEngine(model, max_rows, packed=packed)
         self.max_rows = max_rows
+        self.kv_bits, self.kv_group_size = kv_bits, kv_group_size
 
-    def make_cache(self, capacity: int = 0) -> list[KVCache]:
-        return self.model.make_cache(capacity)
+    def make_cache(self, capacity: int = 0) -> list:
+        """The target's caches: quantized (mlx-lm QuantizedKVCache layout) when the target was
+        built with ``kv_bits`` (target.py:166-184), plain bf16 otherwise."""
+        return self.model.make_cache(capacity, self.kv_bits, self.kv_group_size)
 
     def _fused_rows(self, M: int, tap):
         """The step's tap output as the reference returns it: [1, M, n_tap * H], or None."""

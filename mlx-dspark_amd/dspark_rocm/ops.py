@@ -465,7 +465,7 @@ def verify_attention_blocks(B: int, Hq: int, Hk: int, mq: int, D: int, L: int) -
 
 
 def verify_attention_quantized(q: torch.Tensor, keys, values, *, scale: float, causal: bool = True, bits: int = 8,
-                               group_size: int = GROUP, out: torch.Tensor | None = None,
+                               group_size: int = GROUP, out: torch.Tensor | None = None, out_strides=None,
                                workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Verify attention over a quantized KV cache (mlx-lm ``QuantizedKVCache`` state).
 
@@ -473,6 +473,8 @@ def verify_attention_quantized(q: torch.Tensor, keys, values, *, scale: float, c
     biases [B, Hk, L, D/64]) with scales/biases in q's dtype, fields of ``bits`` (4 or 8)
     along D, low bits first; any batch/head/seq strides (cache views), unit stride along the
     last dim. Semantics: attention over ``scale * q_field + bias`` per group of 64 values.
+    ``out_strides`` = (batch, query head, position) element strides of ``out`` (head_dim
+    contiguous), e.g. [B, Mq, Hq*D] rows for o_proj; default a contiguous [B, Hq, Mq, D].
     """
     kw, ks, kb = keys
     vw, vs, vb = values
@@ -495,8 +497,12 @@ def verify_attention_quantized(q: torch.Tensor, keys, values, *, scale: float, c
         raise ValueError("scales and biases of one cache must share strides")
     q = q.contiguous()
     if out is None:
+        if out_strides is not None:
+            raise ValueError("out_strides needs out")
         out = torch.empty_like(q)
-    osr = (ctypes.c_int64 * 3)(Hq * mq * D, mq * D, D)
+    if out.dtype != q.dtype:
+        raise TypeError(f"out dtype {out.dtype} does not match q's {q.dtype}")
+    osr = (ctypes.c_int64 * 3)(*([Hq * mq * D, mq * D, D] if out_strides is None else [int(x) for x in out_strides]))
     nbytes = _lib.load().dspark_verify_attention_workspace(B, Hq, Hk, mq, D, L)
     ws = _pick(workspace, q.device, nbytes, qmm=False)
     _lib.call("dspark_verify_attention_quantized", dt, _ptr(q), B, Hq, mq, D, _ptr(kw), _ptr(ks), _ptr(kb), _i64x3(kw),
@@ -661,6 +667,33 @@ def qk_norm_rope_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w:
     _lib.call("dspark_qk_norm_rope_kv", _ptr(q), q.stride(0), _ptr(k), k.stride(0), _ptr(v), v.stride(0), M, heads,
               kv_heads, head_dim, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), float(rope_base), int(pos0),
               _ptr(q_out), _ptr(k_cache), ks, _ptr(v_cache), vs, _stream(q))
+    return q_out
+
+
+def qk_norm_rope_kv_quantized(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_w: torch.Tensor,
+                              k_norm_w: torch.Tensor, *, heads: int, kv_heads: int, head_dim: int, eps: float,
+                              rope_base: float, pos0: int, q_out: torch.Tensor, k_cache, v_cache, bits: int,
+                              group_size: int = GROUP) -> torch.Tensor:
+    """:func:`qk_norm_rope_kv` into a quantized cache: ``k_cache`` / ``v_cache`` are the
+    (words [Hk, capacity, D*bits/32], scales [Hk, capacity, D/64], biases) triples of one
+    layer (batch 1, bf16 scales); the rows at pos0.. are quantized as ``quant.quantize_rows``
+    quantizes the values the plain kernel would write."""
+    kw, ks, kb = k_cache
+    vw, vs, vb = v_cache
+    _require_cuda(q, k, v, q_out, kw, ks, kb, vw, vs, vb)
+    for t in (ks, kb, vs, vb):
+        _require_bf16("cache scales / biases", t)
+    M = q.shape[0]
+    for name, t in (("key words", kw), ("value words", vw), ("key scales", ks), ("value scales", vs)):
+        if t.dim() != 3 or t.shape[1] < pos0 + M or t.stride(-1) != 1:
+            raise ValueError(f"{name}: expected [Hk, capacity >= {pos0 + M}, ...] with unit last stride")
+    if ks.stride() != kb.stride() or vs.stride() != vb.stride():
+        raise ValueError("scales and biases of one cache must share strides")
+    two = lambda t: (ctypes.c_int64 * 2)(t.stride(0), t.stride(1))
+    _lib.call("dspark_qk_norm_rope_kv_quantized", _ptr(q), q.stride(0), _ptr(k), k.stride(0), _ptr(v), v.stride(0), M,
+              heads, kv_heads, head_dim, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), float(rope_base), int(pos0),
+              _ptr(q_out), _ptr(kw), _ptr(ks), _ptr(kb), two(kw), two(ks), _ptr(vw), _ptr(vs), _ptr(vb), two(vw),
+              two(vs), int(bits), int(group_size), _stream(q))
     return q_out
 
 

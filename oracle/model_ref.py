@@ -74,9 +74,10 @@ class DenseRef:
     bf16-valued), bits) and norm weights; embed [V, H] fp32 (bf16-valued), or any object whose
     ``[ids]`` returns those rows. ``matmul`` evaluates one projection (default :func:`qmm`)."""
 
-    def __init__(self, cfg: dict, embed, layers: list[dict], norm, lm_head, matmul=None):
+    def __init__(self, cfg: dict, embed, layers: list[dict], norm, lm_head, matmul=None, kv_bits=None):
         self.cfg, self.embed, self.layers, self.norm, self.lm_head = cfg, embed, layers, norm, lm_head
         self.matmul = matmul or qmm
+        self.kv_bits = kv_bits      # quantized caches (target.py:166-184): rows kept as scale * q + bias
         c = cfg
         self.k = [np.zeros((c["kv_heads"], 0, c["head_dim"]), np.float32) for _ in layers]
         self.v = [np.zeros((c["kv_heads"], 0, c["head_dim"]), np.float32) for _ in layers]
@@ -113,6 +114,8 @@ class DenseRef:
             v = qmm(y, L["v"]).reshape(M, Hk, D).transpose(1, 0, 2)
             q = rope(rmsnorm(q, L["q_norm"], eps), pos, c["rope_theta"])
             k = rope(rmsnorm(k, L["k_norm"], eps), pos, c["rope_theta"])
+            if self.kv_bits:
+                k, v = self._kv_quantized(k), self._kv_quantized(v)
             self.k[li] = np.concatenate([self.k[li][:, :self.offset], k], axis=1)
             self.v[li] = np.concatenate([self.v[li][:, :self.offset], v], axis=1)
             att = bf(attention(q[None], self.k[li][None], self.v[li][None], D ** -0.5, causal=True)[0])
@@ -126,6 +129,15 @@ class DenseRef:
         self.fused = np.concatenate(captured, axis=-1) if captured else np.zeros((M, 0), np.float32)
         self.offset += M
         return qmm(rmsnorm(h, self.norm, eps), self.lm_head)
+
+    def _kv_quantized(self, x) -> np.ndarray:
+        """Rows [Hk, M, D] as a quantized cache holds them: quantized in groups of 64 along D
+        with quant_ref's rule, dequantized exactly (float64)."""
+        from .quant_ref import dequantize, quantize
+
+        hk, m, d = x.shape
+        w, s, b = quantize(np.asarray(x, np.float32).reshape(hk * m, d), self.kv_bits)
+        return dequantize(w, s, b, self.kv_bits).reshape(hk, m, d)
 
     def trim(self, n: int) -> None:
         n = min(self.offset, max(0, int(n)))

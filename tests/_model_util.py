@@ -23,7 +23,7 @@ def _lin(l):
     return (l.weight.detach().cpu().numpy().view(np.uint32), _bf(l.scales), _bf(l.biases), l.bits)
 
 
-def to_ref(model, matmul=None, embed=None):
+def to_ref(model, matmul=None, embed=None, kv_bits=None):
     """The numpy oracle (oracle.model_ref.DenseRef) holding the same weights (``embed``: an
     object whose ``[ids]`` gives the embedding rows, instead of a copy of the whole table)."""
     from oracle.model_ref import DenseRef
@@ -39,4 +39,4 @@ def to_ref(model, matmul=None, embed=None):
     cfg = dict(heads=a.num_attention_heads, kv_heads=a.num_key_value_heads, head_dim=a.head_dim,
                eps=a.rms_norm_eps, rope_theta=a.rope_theta)
     table = _bf(model.embed_tokens) if embed is None else embed
-    return DenseRef(cfg, table, layers, _bf(model.norm), _lin(model.lm_head), matmul=matmul)
+    return DenseRef(cfg, table, layers, _bf(model.norm), _lin(model.lm_head), matmul=matmul, kv_bits=kv_bits)

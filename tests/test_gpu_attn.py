@@ -173,10 +173,10 @@ def test_refusals(dev):
 
     from dspark_rocm import _lib, ops
 
-    q = torch.zeros((1, 8, 4, 96), dtype=torch.bfloat16, device=dev)
-    k = torch.zeros((1, 2, 64, 96), dtype=torch.bfloat16, device=dev)
+    q = torch.zeros((1, 8, 4, 100), dtype=torch.bfloat16, device=dev)
+    k = torch.zeros((1, 2, 64, 100), dtype=torch.bfloat16, device=dev)
     with pytest.raises(_lib.DsparkError):
-        ops.verify_attention(q, k, k, scale=0.1)          # head_dim 96 unsupported
+        ops.verify_attention(q, k, k, scale=0.1)          # head_dim 100: not a multiple of 8
     q = torch.zeros((1, 6, 4, 64), dtype=torch.bfloat16, device=dev)
     k = torch.zeros((1, 4, 64, 64), dtype=torch.bfloat16, device=dev)
     with pytest.raises(_lib.DsparkError):

@@ -84,7 +84,7 @@ def test_rope_kernel_frequency_schedule(dev, D, base):
     from dspark_rocm import ops
 
     ones = torch.ones(D, dtype=torch.bfloat16, device=dev)
-    r0 = float(model_ref.bf(np.float32(np.sqrt(D))))
+    r0 = float(model_ref.bf(np.full(1, np.sqrt(D), np.float32))[0])
 
     def rope_fn(x, pos, b):
         p = int(pos[0])
@@ -278,8 +278,10 @@ def test_verify_tap_returns_the_tapped_hidden_states(dev):
     after each tapped layer in layer order, whatever the order, duplicates or out-of-range
     entries of ``tap`` (target.py:208-220, :642-677). The tap changes no logit bit; each column
     block is bitwise the block a one-layer tap returns; against the oracle's tapped forward and
-    the module path's capture within 2e-2 x RMS per block; ``tap=None`` returns None; the
-    prefill chunk returns the same capture through the module path (target.py:435-465)."""
+    the module path's capture within the multi-layer forward's bar per block (5e-2 x RMS, as
+    for the logits: the stream is bf16 after every layer, and one ulp of its largest values is
+    ~3% of its RMS); ``tap=None`` returns None; the prefill chunk returns the same capture
+    through the module path (target.py:435-465)."""
     from dspark_rocm.model import Target, tap_layers
 
     model = tiny_model(dev, seed=13, num_hidden_layers=4)
@@ -310,28 +312,29 @@ def test_verify_tap_returns_the_tapped_hidden_states(dev):
     want = ref.fused
     assert want.shape == (12, 2 * H)
     for j in range(2):
-        assert_rms_close(_np(fused[0, :, j * H:(j + 1) * H]), want[:, j * H:(j + 1) * H], 2e-2, f"tap block {j}")
+        assert_rms_close(_np(fused[0, :, j * H:(j + 1) * H]), want[:, j * H:(j + 1) * H], 5e-2, f"tap block {j}")
     # the module path (Target.run) and a prefill chunk capture the same stream
     cm = tgt.make_cache(64)
     tgt.prefill(torch.tensor([prefix]), cm)
     with torch.no_grad():
         logits_m, fused_m = tgt.run(torch.tensor([block]), cm, tap)
     assert fused_m.shape == fused.shape
-    assert_rms_close(_np(fused_m[0]), _np(fused[0]), 2e-2, "module path capture")
+    assert_rms_close(_np(fused_m[0]), _np(fused[0]), 5e-2, "module path capture")
     cp = tgt.make_cache(64)
     with torch.no_grad():
         none, fused_p = tgt.prefill(torch.tensor([prefix + block]), cp, tap)
         lp, nofused = tgt.prefill(torch.tensor([block[:3]]), cp, want_logits=True)
     assert none is None and nofused is None and lp.shape == (1, 1, model.args.vocab_size)
     assert fused_p.shape == (1, 32, 2 * H)
-    assert_rms_close(_np(fused_p[0, 20:]), want, 2e-2, "prefill capture")
+    assert_rms_close(_np(fused_p[0, 20:]), want, 5e-2, "prefill capture")
 
 
 def test_speculative_trace_feeds_the_drafter_its_context_rows(dev):
     """The DSpark loop's context update (generate.py:1547, :1590-1593): every round hands
     fused[:, :n + 1] (the tapped states of [pending, accepted drafts]) to the drafter. A stub
     update_context checks each call's shape and offset; over the whole trace the rows it
-    received are the oracle's tapped stream over the committed tokens, position for position."""
+    received are the oracle's tapped stream over the committed tokens, position for position
+    (within the multi-layer forward's 5e-2 x RMS bar)."""
     from dspark_rocm.model import Target
 
     model = tiny_model(dev, seed=15, num_hidden_layers=3)
@@ -363,7 +366,7 @@ def test_speculative_trace_feeds_the_drafter_its_context_rows(dev):
     ref.forward(prompt + out[:-1], tap=tap)
     want = ref.fused[len(prompt):]
     assert got.shape == want.shape
-    assert_rms_close(_np(got), want, 2e-2, "context rows over the trace")
+    assert_rms_close(_np(got), want, 5e-2, "context rows over the trace")
 
 
 def test_packed_engine_is_bitwise_the_reference_layout_engine(dev):

@@ -120,3 +120,20 @@ def test_c_matmul_and_seeded_cache_agree_with_the_numpy_forward():
     seeded.seed_cache([k[:, :5] for k in full.k], [v[:, :5] for v in full.v])
     assert seeded.offset == 5
     assert np.array_equal(seeded.forward([42, 7]), full.forward([42, 7]))
+
+
+def test_quantized_kv_forward_matches_torch_module_path_on_cpu():
+    """The oracle's quantized-cache forward (rows quantized with quant_ref's rule, dequantized
+    exactly) against the torch module path over QuantizedKVCache on the CPU (quant.quantize_rows,
+    then the stock quantized SDPA): two implementations of the same cache semantics. Bar: the
+    whole forward's 5e-2 x RMS (a key that rounds to a neighbouring field moves by a whole
+    quantization step, which the two-layer forward then carries)."""
+    for bits in (8, 4):
+        model = tiny_model("cpu", seed=17)
+        ref = to_ref(model, kv_bits=bits)
+        cache = model.make_cache(64, kv_bits=bits)
+        for ids in ([5, 17, 200, 3, 99, 41], [7, 8, 9]):
+            with torch.no_grad():
+                got = model(torch.tensor([ids]), cache)[0].float().numpy()
+            want = ref.forward(ids)
+            assert np.abs(got - want).max() <= 5e-2 * np.sqrt(np.mean(want.astype(np.float64) ** 2)), bits
