@@ -1,29 +1,31 @@
-"""Load-time wiring of the verify kernels: measure each shape's gate once per machine, cache the
-verdict, and turn the kernels on for a loaded target (and drafter).
+"""Load-time wiring of the verify kernels: each kernel's gate is measured once per machine, the
+verdict is cached on disk, and the process-wide settings that the dispatch scopes read are set
+from it for a loaded target (and drafter).
 
-The reference's entry points (calibrate.py:1062-1153 for the small-M qmm, :1352-1407 for the
-multi-row attention):
+Entry points (names, signatures and meaning as the reference's calibrate.py:933-985,
+:1062-1153, :1222-1302, :1352-1407):
 
-* ``small_m_qmm_shapes(target, drafter, target_repo=...)`` -> the weight-shape keys whose
-  kernel passes :func:`dspark_rocm.small_m_qmm.measure_shapes` here; ``apply_small_m`` turns
-  them into the instance allowlist and stores it in :data:`SMALL_M_IDS`.
-* ``multirow_windows(shapes)`` -> one measured :class:`~dspark_rocm.multirow_attn.Window`
-  per attention shape; ``apply_multirow_attn(target, drafter)`` finds the target's and a DSpark
-  drafter's attention shapes, measures them and stores the config in :data:`MULTIROW_CFG`.
-* ``wide_gemm_min_rows`` / ``apply_wide_gemm(target, drafter)`` measure the prefill wide
-  path's crossover and verified shapes (:mod:`dspark_rocm.wide_gemm`) and store them in
-  :data:`WIDE_GEMM_MIN_ROWS` / :data:`WIDE_GEMM_SHAPES`, which ``Target.prefill`` reads
-  (calibrate.py:933-985).
-* :func:`verify_scopes` enters the scopes a verify loop runs under, in the reference's order
-  (generate.py:52-83): the row split outermost, the multi-row attention inside it (so calls it
-  does not serve fall through to the split), then the small-M allowlist.
+* ``small_m_qmm_shapes`` / ``apply_small_m`` -- the weight-shape keys whose small-M kernel
+  passes :func:`dspark_rocm.small_m_qmm.measure_shapes`, turned into the instance allowlist
+  :data:`SMALL_M_IDS`;
+* ``multirow_windows`` / ``apply_multirow_attn`` -- one measured
+  :class:`~dspark_rocm.multirow_attn.Window` per attention shape (the target's and a DSpark
+  drafter's context attention), stored as :data:`MULTIROW_CFG`;
+* ``measure_split_window`` / ``apply_sdpa_split`` -- the row-split window of the stock
+  attention path (:data:`SDPA_SPLIT_CFG`), on only where splitting a wide verify call is
+  measured to be faster;
+* ``wide_gemm_min_rows`` / ``apply_wide_gemm`` -- the prefill wide path's crossover and
+  verified shapes (:data:`WIDE_GEMM_MIN_ROWS` / :data:`WIDE_GEMM_SHAPES`);
+* :func:`verify_scopes` -- the scopes a verify loop runs under, in the reference's order
+  (generate.py:52-83): row split outermost, multi-row attention inside it (calls it does not
+  serve fall through to the split), then the small-M allowlist.
 
-Verdicts are cached as JSON, one file per key, keyed by the GPU (name and gfx target) and this
-library's version, so a machine measures once. A cached shape list that matches no live module
-(a shape-key format change) is measured again (calibrate.py:1136-1150). Nothing here raises on a
-kernel failure: a shape that cannot run stays on the stock path. (The reference also gates both
-kernels by Apple GPU generation, calibrate.py:1053-1059 and :1311-1314; MI355X has no such
-gate.)
+Every measurement goes through one helper, :func:`verdict`: a :class:`Probe` names what is
+measured (its kind and subject), how, how to report it, and when a cached value no longer
+describes the live models. Verdicts are JSON files keyed by the GPU (name, gfx target) and this
+library's version. Nothing here raises on a kernel failure: a shape that cannot run stays on
+the stock path. (The reference also gates kernels by Apple GPU generation, calibrate.py:1053-1059
+and :1311-1314; MI355X has no such gate.)
 """
 
 from __future__ import annotations
@@ -32,6 +34,8 @@ import contextlib
 import hashlib
 import json
 import os
+from dataclasses import dataclass
+from typing import Any, Callable
 
 SCHEMA = 1
 
@@ -91,24 +95,59 @@ def device_key() -> str:
     return f"v{SCHEMA}|{dev}|{lib}"
 
 
+@dataclass(frozen=True)
+class Probe:
+    """One cached measurement: ``kind`` and ``subject`` make its cache key; ``measure()``
+    returns a JSON-serialisable value; ``report(value)`` says what it means for the log;
+    ``stale(value)`` tells a cached value that no longer fits the live models (measured again)."""
+    kind: str
+    subject: str
+    measure: Callable[[], Any]
+    report: Callable[[Any], str]
+    stale: Callable[[Any], bool] = lambda value: False
+
+
+def verdict(probe: Probe, *, cache_dir: str | None = None, refresh: bool = False, verbose: bool = True):
+    """The probe's value: cached for this GPU and library when present and not stale, else
+    measured now and cached (``refresh`` always measures)."""
+    key = f"{device_key()}|{probe.kind}|{probe.subject}"
+    value = None if refresh else load_cached(key, cache_dir)
+    if value is not None and not probe.stale(value):
+        return value
+    if verbose:
+        print(f"measuring {probe.kind} for {probe.subject} (once on this machine, then cached)", flush=True)
+    value = probe.measure()
+    save_cached(key, value, cache_dir)
+    if verbose:
+        print(f"  {probe.kind}: {probe.report(value)}", flush=True)
+    return value
+
+
+def _model_of(obj):
+    """The network inside a Target-like wrapper (``.model``), or the object itself."""
+    return getattr(obj, "model", obj)
+
+
 # ------------------------------------------------------------------ small-M qmm
+
+def _small_m_probe(target, drafter, target_repo, drafter_repo) -> Probe:
+    from . import small_m_qmm
+
+    model = _model_of(target)
+    return Probe(
+        "smallm", f"{target_repo}|{drafter_repo}",
+        measure=lambda: list(small_m_qmm.measure_shapes(model, drafter, verbose=False)),
+        report=lambda keys: f"{len(keys)} weight shapes take the kernel" if keys else "every shape stays stock",
+        # keys written under another key format match no live module (calibrate.py:1136-1150)
+        stale=lambda keys: bool(keys) and not small_m_qmm.ids_for_shapes(keys, model, drafter))
+
 
 def small_m_qmm_shapes(target, drafter=None, *, target_repo: str, drafter_repo: str | None = None,
                        cache_dir: str | None = None, refresh: bool = False, verbose: bool = True) -> list[str]:
     """Weight-shape keys whose verify-window forwards should run on the small-M kernel here,
     measured once and cached (``refresh`` measures again and overwrites)."""
-    from . import small_m_qmm
-
-    key = f"{device_key()}|smallm|{target_repo}|{drafter_repo}"
-    shapes = None if refresh else load_cached(key, cache_dir)
-    if shapes is None:
-        if verbose:
-            print("calibrating the small-M qmm kernel (once per machine, cached)", flush=True)
-        shapes = small_m_qmm.measure_shapes(getattr(target, "model", target), drafter, verbose=verbose)
-        save_cached(key, shapes, cache_dir)
-        if verbose:
-            print(f"  small-M qmm: {'on for ' + str(len(shapes)) + ' weight shapes' if shapes else 'off'}", flush=True)
-    return list(shapes)
+    probe = _small_m_probe(target, drafter, target_repo, drafter_repo)
+    return list(verdict(probe, cache_dir=cache_dir, refresh=refresh, verbose=verbose))
 
 
 def apply_small_m(target, drafter=None, *, target_repo: str, drafter_repo: str | None = None,
@@ -118,70 +157,73 @@ def apply_small_m(target, drafter=None, *, target_repo: str, drafter_repo: str |
     global SMALL_M_IDS
     from .small_m_qmm import ids_for_shapes
 
-    if enabled is False:
-        SMALL_M_IDS = None
-        return None
-    model = getattr(target, "model", target)
-    kw = dict(target_repo=target_repo, drafter_repo=drafter_repo, cache_dir=cache_dir, verbose=verbose)
-    shapes = small_m_qmm_shapes(target, drafter, **kw)
-    ids = ids_for_shapes(shapes, model, drafter)
-    if shapes and not ids:
-        # the cached keys match no live module: written under another shape-key format
-        shapes = small_m_qmm_shapes(target, drafter, refresh=True, **kw)
-        ids = ids_for_shapes(shapes, model, drafter)
-    SMALL_M_IDS = ids or None
+    SMALL_M_IDS = None
+    if enabled is not False:
+        keys = small_m_qmm_shapes(target, drafter, target_repo=target_repo, drafter_repo=drafter_repo,
+                                  cache_dir=cache_dir, verbose=verbose)
+        SMALL_M_IDS = ids_for_shapes(keys, _model_of(target), drafter) or None
     return SMALL_M_IDS
 
 
-# ------------------------------------------------------------------ multi-row attention
+# ------------------------------------------------------------------ attention shapes
 
 def _attn_dims(target):
     """(query heads, KV heads, head dim) of the target's attention layers, or None."""
-    model = getattr(target, "model", target)
-    args = getattr(model, "args", None)
+    args = getattr(_model_of(target), "args", None)
     if args is None:
         return None
-    if isinstance(args, dict):
-        get = args.get
-    else:
-        def get(k, default=None):
-            return getattr(args, k, default)
-    hq, hk = get("num_attention_heads"), get("num_key_value_heads") or get("num_attention_heads")
-    d = get("head_dim") or (get("hidden_size") // hq if hq and get("hidden_size") else None)
+    field = args.get if isinstance(args, dict) else (lambda name: getattr(args, name, None))
+    hq = field("num_attention_heads")
+    hk = field("num_key_value_heads") or hq
+    width = field("hidden_size")
+    d = field("head_dim") or (width // hq if hq and width else None)
     return (int(hq), int(hk), int(d)) if hq and hk and d else None
+
+
+# what keeps a DSpark drafter's context attention off the kernel: a causal block, a sliding
+# window or attention sinks (its calls then carry array masks), or no context update at all
+# (calibrate.py:1315-1327)
+_DRAFTER_BLOCKERS = ("causal_block", "sliding_window", "sink")
+_DRAFTER_NEEDS = ("n_heads", "n_kv_heads", "head_dim", "update_ctx")
 
 
 def _drafter_attn_dims(drafter):
     """(query heads, KV heads, head dim) of a DSpark drafter's context attention when it can
-    take the kernel (an unmasked block without sinks: no causal block, sliding window or sink,
-    and a context update), else None (calibrate.py:1315-1327)."""
-    layers = getattr(drafter, "layers", None) or []
-    attn = getattr(layers[0], "self_attn", None) if len(layers) else None
-    if attn is None or not all(hasattr(attn, n) for n in ("n_heads", "n_kv_heads", "head_dim", "update_ctx")):
+    take the kernel, else None."""
+    layers = list(getattr(drafter, "layers", None) or [])
+    attn = getattr(layers[0], "self_attn", None) if layers else None
+    if attn is None or not all(hasattr(attn, n) for n in _DRAFTER_NEEDS):
         return None
-    if getattr(attn, "causal_block", False) or getattr(attn, "sliding_window", None) or getattr(attn, "sink", False):
+    if any(getattr(attn, n, None) for n in _DRAFTER_BLOCKERS):
         return None
     return int(attn.n_heads), int(attn.n_kv_heads), int(attn.head_dim)
 
 
+def _attention_shapes(target, drafter) -> list[tuple[int, int, int]]:
+    """The distinct attention shapes of the target and a DSpark drafter, target first."""
+    found = (_attn_dims(target), _drafter_attn_dims(drafter) if drafter is not None else None)
+    return list(dict.fromkeys(s for s in found if s))
+
+
+# ------------------------------------------------------------------ multi-row attention
+
 def multirow_windows(shapes, *, cache_dir: str | None = None, refresh: bool = False, verbose: bool = True) -> list:
     """One measured :class:`~dspark_rocm.multirow_attn.Window` per (hq, hk, d) that wins here
     (each raced and checked once, cached)."""
-    from .multirow_attn import Window, measure_window
+    from . import multirow_attn
 
-    out = []
-    for hq, hk, d in shapes:
-        key = f"{device_key()}|multirow|{hq}x{hk}x{d}"
-        hit = None if refresh else load_cached(key, cache_dir)
-        if hit is None:
-            if verbose:
-                print(f"calibrating multi-row attention for {hq}x{hk}x{d} (once per machine, cached)", flush=True)
-            win, report = measure_window(hq, hk, d, verbose=verbose)
-            hit = {"window": win, "report": report}
-            save_cached(key, hit, cache_dir)
-        if hit.get("window"):
-            out.append(Window(hq, hk, d, **hit["window"]))
-    return out
+    def probe(hq, hk, d):
+        def measure():
+            window, report = multirow_attn.measure_window(hq, hk, d, verbose=False)
+            return {"window": window, "report": report}
+
+        return Probe("multirow", f"{hq}x{hk}x{d}", measure,
+                     report=lambda v: (f"q {v['window']['min_q']}..{v['window']['max_q']} from "
+                                       f"{v['window']['min_kv']} keys" if v.get("window") else
+                                       f"stock ({(v.get('report') or {}).get('reason', 'no win')})"))
+
+    measured = [(s, verdict(probe(*s), cache_dir=cache_dir, refresh=refresh, verbose=verbose)) for s in shapes]
+    return [multirow_attn.Window(*s, **v["window"]) for s, v in measured if v.get("window")]
 
 
 def apply_multirow_attn(target, drafter=None, *, enabled: bool | None = None, cache_dir: str | None = None,
@@ -191,16 +233,105 @@ def apply_multirow_attn(target, drafter=None, *, enabled: bool | None = None, ca
     global MULTIROW_CFG
     from .multirow_attn import MultirowConfig
 
-    if enabled is False:
-        MULTIROW_CFG = None
-        return None
-    shapes = []
-    for dims in (_attn_dims(target), _drafter_attn_dims(drafter) if drafter is not None else None):
-        if dims and dims not in shapes:
-            shapes.append(dims)
-    windows = multirow_windows(shapes, cache_dir=cache_dir, verbose=verbose)
-    MULTIROW_CFG = MultirowConfig(tuple(windows)) if windows else None
+    MULTIROW_CFG = None
+    if enabled is not False:
+        windows = multirow_windows(_attention_shapes(target, drafter), cache_dir=cache_dir, verbose=verbose)
+        MULTIROW_CFG = MultirowConfig(tuple(windows)) if windows else None
     return MULTIROW_CFG
+
+
+# ------------------------------------------------------------------ row split of the stock path
+
+SPLIT_PROBE_KEYS = 16384      # keys of the probe's synthetic cache
+SPLIT_MARGIN = 0.05           # a split width must save at least this fraction of the call
+
+
+def split_window_from_costs(cost: dict, max_chunk: int, *, min_kv: int = 4096,
+                            margin: float = SPLIT_MARGIN) -> dict | None:
+    """The split window a cost sweep implies (``cost[q]`` = one stock call of q rows), or None.
+
+    Width q gains when the blocks :func:`sdpa_split._partition` cuts it into cost, together,
+    less than ``(1 - margin) * cost[q]``. The window is the first run of consecutive gaining
+    widths above ``max_chunk`` (a lone gain after a gap is timing noise)."""
+    from .sdpa_split import _partition
+
+    def gains(q):
+        return q in cost and sum(cost[s] for s in _partition(q, max_chunk)) < (1.0 - margin) * cost[q]
+
+    q = max_chunk + 1
+    top = max(cost) if cost else 0
+    while q <= top and not gains(q):
+        q += 1
+    if q > top:
+        return None
+    first = q
+    while q + 1 <= top and gains(q + 1):
+        q += 1
+    return {"min_q": first, "max_q": q, "min_kv": min_kv, "max_chunk": max_chunk}
+
+
+def _stock_attention_costs(hq: int, hk: int, d: int, widths=range(1, 17), keys: int = SPLIT_PROBE_KEYS) -> dict:
+    """Milliseconds of one stock attention call per q_len (causal, bf16, over ``keys`` keys;
+    HIP events over back-to-back calls rotating two KV sets)."""
+    import torch
+
+    from . import fast, gate
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(hq * 131 + d)
+    kv = [(torch.randn((1, hk, keys, d), generator=g, device=dev).to(torch.bfloat16),
+           torch.randn((1, hk, keys, d), generator=g, device=dev).to(torch.bfloat16)) for _ in range(2)]
+    out = {}
+    for q_len in widths:
+        q = torch.randn((1, hq, q_len, d), generator=g, device=dev).to(torch.bfloat16)
+        calls = [lambda k=k, v=v: fast.STOCK(q, k, v, scale=d ** -0.5, mask="causal") for k, v in kv]
+        out[q_len] = min(gate.chain_ms(calls) for _ in range(3))
+    return out
+
+
+def _split_chunk(cost: dict, limit: int = 8) -> int:
+    """The block size of the split: the width up to ``limit`` with the lowest cost per row (the
+    stock path's most efficient width on this machine)."""
+    candidates = [q for q in cost if q <= limit]
+    return min(candidates, key=lambda q: (cost[q] / q, -q)) if candidates else 1
+
+
+def measure_split_window(hq: int, hk: int, d: int, *, cache_dir: str | None = None, refresh: bool = False,
+                         verbose: bool = True) -> dict | None:
+    """The row-split window ``{min_q, max_q, min_kv, max_chunk}`` of the stock attention path
+    for this shape on this machine, or None where splitting never pays (cached)."""
+    def measure():
+        try:
+            cost = _stock_attention_costs(hq, hk, d)
+        except Exception as e:  # noqa: BLE001 - no device or no memory: the split stays off
+            return {"window": None, "reason": f"{type(e).__name__}: {e}"}
+        return {"window": split_window_from_costs(cost, _split_chunk(cost)), "cost_ms": cost}
+
+    probe = Probe("split", f"{hq}x{hk}x{d}", measure,
+                  report=lambda v: (f"rows {v['window']['min_q']}..{v['window']['max_q']} in blocks of "
+                                    f"{v['window']['max_chunk']}" if v.get("window") else "no gain: off"))
+    return verdict(probe, cache_dir=cache_dir, refresh=refresh, verbose=verbose).get("window")
+
+
+def apply_sdpa_split(target, *, target_repo: str | None = None, enabled: bool | None = None,
+                     cache_dir: str | None = None, verbose: bool = True):
+    """Turn the row split of the stock attention path on for this process
+    (:data:`SDPA_SPLIT_CFG`) and return its :class:`~dspark_rocm.sdpa_split.SplitConfig`, or
+    None when off. ``enabled=None`` measures (cached); False disables; True takes the default
+    window without measuring, as does a target whose attention shape cannot be read."""
+    global SDPA_SPLIT_CFG
+    from .sdpa_split import SplitConfig
+
+    dims = _attn_dims(target) if enabled is None else None
+    if enabled is False:
+        SDPA_SPLIT_CFG = None
+    elif enabled is True or dims is None:
+        SDPA_SPLIT_CFG = SplitConfig()
+    else:
+        window = measure_split_window(*dims, cache_dir=cache_dir, verbose=verbose)
+        SDPA_SPLIT_CFG = SplitConfig(**window) if window else None
+    return SDPA_SPLIT_CFG
 
 
 # ------------------------------------------------------------------ prefill wide path
@@ -210,26 +341,22 @@ def wide_gemm_min_rows(target, drafter=None, *, target_repo: str, cache_dir: str
     """``(min_rows, shape keys)`` from which prefill forwards take the wide path here, or
     ``(None, [])`` when it never pays or no shape verifies; measured once (the drafter's
     projections run at prefill width too, so its shapes are verified with the target's) and
-    cached (calibrate.py:933-962)."""
-    from .wide_gemm import measure_crossover
+    cached."""
+    from . import wide_gemm
 
-    key = f"{device_key()}|widegemm|{target_repo}"
-    entry = None if refresh else load_cached(key, cache_dir)
-    if entry is None:
-        if verbose:
-            print("calibrating the prefill wide path (once per machine, cached)", flush=True)
+    def measure():
         try:
-            got = measure_crossover(getattr(target, "model", target), drafter)
+            found = wide_gemm.measure_crossover(_model_of(target), drafter)
         except Exception as e:  # noqa: BLE001 - a kernel that will not launch leaves prefill on stock
-            if verbose:
-                print(f"  prefill wide path: off (kernel unavailable: {type(e).__name__}: {e})", flush=True)
-            got = None
-        entry = {"min_rows": got[0], "shapes": got[1]} if got else {"min_rows": None, "shapes": []}
-        save_cached(key, entry, cache_dir)
-        if verbose:
-            state = (f"on from M={entry['min_rows']} for {len(entry['shapes'])} weight shapes (verified bit-identical)"
-                     if entry["min_rows"] else "off (no gain, or not exact here)")
-            print(f"  prefill wide path: {state}", flush=True)
+            return {"min_rows": None, "shapes": [], "reason": f"{type(e).__name__}: {e}"}
+        min_rows, shapes = found if found else (None, [])
+        return {"min_rows": min_rows, "shapes": list(shapes)}
+
+    probe = Probe("widegemm", target_repo, measure,
+                  report=lambda v: (f"prefill projections of >= {v['min_rows']} rows, {len(v['shapes'])} shapes, "
+                                    "bit-identical to stock" if v.get("min_rows") else
+                                    f"stock ({v.get('reason', 'never faster, or no shape exact')})"))
+    entry = verdict(probe, cache_dir=cache_dir, refresh=refresh, verbose=verbose)
     return entry.get("min_rows"), list(entry.get("shapes") or [])
 
 
@@ -237,17 +364,18 @@ def apply_wide_gemm(target, drafter=None, *, target_repo: str, min_rows: int | N
                     cache_dir: str | None = None, verbose: bool = True) -> int | None:
     """Turn the prefill wide path on for this process (:data:`WIDE_GEMM_MIN_ROWS`,
     :data:`WIDE_GEMM_SHAPES`) and return the threshold. ``min_rows=None`` measures (cached),
-    0 disables, N forces N -- still only for the shapes that verify at N (calibrate.py:965-985)."""
+    0 disables, N forces N -- raised to the path's floor and still only for the shapes that
+    verify there."""
     global WIDE_GEMM_MIN_ROWS, WIDE_GEMM_SHAPES
-    from .wide_gemm import SAFE_MIN_ROWS, verified_shapes
+    from . import wide_gemm
 
     if min_rows is None:
         WIDE_GEMM_MIN_ROWS, WIDE_GEMM_SHAPES = wide_gemm_min_rows(target, drafter, target_repo=target_repo,
                                                                   cache_dir=cache_dir, verbose=verbose)
-    else:
-        WIDE_GEMM_MIN_ROWS = max(int(min_rows), SAFE_MIN_ROWS) if int(min_rows) else None
-        WIDE_GEMM_SHAPES = (verified_shapes([getattr(target, "model", target), drafter], WIDE_GEMM_MIN_ROWS)
-                            if WIDE_GEMM_MIN_ROWS else [])
+        return WIDE_GEMM_MIN_ROWS
+    forced = max(int(min_rows), wide_gemm.SAFE_MIN_ROWS) if int(min_rows) else None
+    WIDE_GEMM_MIN_ROWS = forced
+    WIDE_GEMM_SHAPES = wide_gemm.verified_shapes([_model_of(target), drafter], forced) if forced else []
     return WIDE_GEMM_MIN_ROWS
 
 

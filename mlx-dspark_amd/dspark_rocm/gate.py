@@ -52,3 +52,13 @@ class Bar:
 
     def met(self, ratio: float) -> bool:
         return ratio >= self.min_speedup
+
+
+def winning_tail(wins: Sequence[bool]) -> int | None:
+    """Index where the run of wins that reaches the end of ``wins`` begins (a sweep ordered by
+    size: the smallest size from which the kernel keeps winning), or None when the last entry
+    loses."""
+    start = len(wins)
+    while start > 0 and wins[start - 1]:
+        start -= 1
+    return start if start < len(wins) else None

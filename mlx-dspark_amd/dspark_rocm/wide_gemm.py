@@ -127,102 +127,93 @@ def active() -> bool:
 
 # ------------------------------------------------------------------ calibration
 
+def _network(model):
+    """Where a model keeps its modules: a wrapper holding its network as ``.model`` is searched
+    there (wide_gemm.py:235-244)."""
+    return getattr(model, "model", model)
+
+
 def quantized_linears(*models):
-    """Every eligible ``QuantizedLinear`` in the given models (target, drafter, ...); a model
-    holding its network as ``.model`` is searched there (wide_gemm.py:235-244)."""
-    for model in models:
-        if model is None:
-            continue
-        inner = getattr(model, "model", model)
-        if not hasattr(inner, "modules"):
-            continue
-        for mod in inner.modules():
-            if _eligible(mod):
-                yield mod
+    """Every eligible ``QuantizedLinear`` in the given models (target, drafter, ...), model by
+    model in module order."""
+    for net in (_network(m) for m in models if m is not None):
+        if hasattr(net, "modules"):
+            yield from filter(_eligible, net.modules())
 
 
 def widest_quantized_linear(*models):
-    """The eligible ``QuantizedLinear`` with the most weight words (the MLP projections that
-    dominate prefill), or None for a model with none (wide_gemm.py:247-251)."""
-    best, best_size = None, 0
-    for mod in quantized_linears(*models):
-        if mod.weight.numel() > best_size:
-            best, best_size = mod, mod.weight.numel()
-    return best
+    """The eligible ``QuantizedLinear`` with the most weight words, the first of equals (the MLP
+    projections that dominate prefill), or None for models without one (wide_gemm.py:247-251)."""
+    return max(quantized_linears(*models), key=lambda mod: mod.weight.numel(), default=None)
 
 
 def _probe_x(mod, M: int, gen: torch.Generator) -> torch.Tensor:
     return torch.randn((M, _in_features(mod)), generator=gen, device=mod.weight.device).to(mod.scales.dtype)
 
 
-def _matches(mod, M: int, exact: bool = True, seed: int = 0) -> bool:
-    """Do the stock and wide paths agree for this weight at ``M`` rows (bit for bit, or within
-    the bar for ``exact=False``)? Two draws: one lucky match proves little (wide_gemm.py:262-280)."""
+def _agrees(mod, M: int, exact: bool = True, seed: int = 0, draws: int = 2) -> bool:
+    """Whether the wide path gives the stock path's result for this weight at ``M`` rows on
+    ``draws`` random inputs: bit for bit, or (``exact=False``) within the qmm bar. One lucky
+    match proves little, hence two draws by default (wide_gemm.py:262-280)."""
     gen = torch.Generator(device=mod.weight.device)
     gen.manual_seed(seed + M)
-    for _ in range(2):
+
+    def one_draw() -> bool:
         x = _probe_x(mod, M, gen)
-        a = _orig_call(mod, x)
-        c = wide_rows(mod, x, exact=exact)
-        if a.shape != c.shape or not bool(torch.isfinite(c.float()).all()):
+        stock, wide = _orig_call(mod, x), wide_rows(mod, x, exact=exact)
+        if stock.shape != wide.shape or not bool(torch.isfinite(wide.float()).all()):
             return False
         if exact:
-            if not torch.equal(a, c):
-                return False
-        elif not gate.max_abs_diff(a, c) <= REL_TOL * max(float(a.float().abs().max()), 1.0):
-            return False
-    return True
+            return torch.equal(stock, wide)
+        return gate.max_abs_diff(stock, wide) <= REL_TOL * max(float(stock.float().abs().max()), 1.0)
+
+    return all(one_draw() for _ in range(draws))
+
+
+def _verifies(mod, rows, exact: bool) -> bool:
+    try:
+        return all(_agrees(mod, M, exact) for M in rows)
+    except Exception:  # noqa: BLE001 - a shape the kernel refuses stays on the stock path
+        return False
 
 
 def verified_shapes(models, min_rows: int, widths: tuple[int, ...] = (512, 1024, 2048), *,
                     exact: bool = True) -> list[str]:
     """Shape keys across ``models`` whose wide path agrees with the stock path at ``min_rows``
-    and at each of ``widths`` (wide_gemm.py:283-306): the per-shape allowlist of the scope."""
-    ok: list[str] = []
-    seen: set[str] = set()
+    and at each of ``widths``, checked once per key on its first module, in first-seen order
+    (wide_gemm.py:283-306): the per-shape allowlist of the scope."""
+    first: dict[str, object] = {}
     for mod in quantized_linears(*models):
-        key = shape_key(mod)
-        if key in seen:
-            continue
-        seen.add(key)
-        try:
-            if all(_matches(mod, M, exact) for M in (min_rows, *widths)):
-                ok.append(key)
-        except Exception:  # noqa: BLE001 - a shape the kernel refuses stays on the stock path
-            continue
-    return ok
+        first.setdefault(shape_key(mod), mod)
+    rows = (min_rows, *widths)
+    return [key for key, mod in first.items() if _verifies(mod, rows, exact)]
 
 
-def _ms(fn, repeat: int = 3) -> float:
-    return min(gate.chain_ms([fn], repeat) for _ in range(3))
+def _wide_wins(lin, M: int, gen: torch.Generator, exact: bool, margin: float) -> bool:
+    """Whether the wide path beats the stock path by ``margin`` at ``M`` rows (HIP events over
+    back-to-back calls, best of three)."""
+    x = _probe_x(lin, M, gen)
+    t_stock = min(gate.chain_ms([lambda: _orig_call(lin, x)]) for _ in range(3))
+    t_wide = min(gate.chain_ms([lambda: wide_rows(lin, x, exact=exact)]) for _ in range(3))
+    return t_stock > t_wide * (1.0 + margin)
 
 
 def measure_crossover(*models, widths: tuple[int, ...] = (256, 512, 1024, 2048), margin: float = 0.02,
                       exact: bool = True) -> tuple[int, list[str]] | None:
     """``(min_rows, verified shape keys)`` for this machine and models, or None when the path
-    stays off (nothing quantized, never faster, or no shape verifies) (wide_gemm.py:337-376).
+    stays off: nothing quantized, never faster, or no shape verifies (wide_gemm.py:337-376).
 
-    ``min_rows`` is the smallest measured width from which the wide path beats the stock path
-    by ``margin`` on the widest weight and keeps winning at every wider width; the shapes are
-    those that verify there and at the wider widths. Timing is HIP events over back-to-back
-    calls."""
+    The widest weight is raced at every width (widths under :data:`SAFE_MIN_ROWS` never take the
+    path); ``min_rows`` is where the run of winning widths that reaches the widest one starts,
+    and the shapes are those that verify there and at every wider width."""
     lin = widest_quantized_linear(*models)
     if lin is None:
         return None
     gen = torch.Generator(device=lin.weight.device)
     gen.manual_seed(1)
-    wins: dict[int, bool] = {}
-    for M in widths:
-        if M < SAFE_MIN_ROWS:
-            wins[M] = False
-            continue
-        x = _probe_x(lin, M, gen)
-        t_stock = _ms(lambda: _orig_call(lin, x))
-        t_wide = _ms(lambda: wide_rows(lin, x, exact=exact))
-        wins[M] = t_stock > t_wide * (1.0 + margin)
-    for i, M in enumerate(widths):
-        if not all(wins[m] for m in widths[i:]):
-            continue
-        keys = verified_shapes(models, int(M), widths=tuple(widths[i + 1:]), exact=exact)
-        return (int(M), keys) if keys else None
-    return None
+    wins = [M >= SAFE_MIN_ROWS and _wide_wins(lin, M, gen, exact, margin) for M in widths]
+    start = gate.winning_tail(wins)
+    if start is None:
+        return None
+    keys = verified_shapes(models, int(widths[start]), widths=tuple(widths[start + 1:]), exact=exact)
+    return (int(widths[start]), keys) if keys else None

@@ -183,3 +183,42 @@ def test_wide_gemm_threshold_measured_once_and_forced_threshold_verifies(cal, mo
     assert seen == [wide_gemm.SAFE_MIN_ROWS] and cal.WIDE_GEMM_SHAPES == ["k2"]  # verified at the clamped width
     assert cal.apply_wide_gemm(model, target_repo="t", min_rows=0, verbose=False) is None
     assert cal.WIDE_GEMM_SHAPES == []
+
+
+def test_split_window_from_costs_kats(cal):
+    """The window a stock-path cost sweep implies: widths whose balanced blocks cost together
+    less than 95% of one call, the first consecutive run above the block size."""
+    flat = {q: 1.0 for q in range(1, 17)}                         # cost independent of width: no gain
+    assert cal.split_window_from_costs(flat, 4) is None
+    linear = {q: float(q) for q in range(1, 17)}                  # cost per row constant: blocks never gain
+    assert cal.split_window_from_costs(linear, 4) is None
+    cliff = {q: (1.0 if q <= 5 else 6.0) for q in range(1, 17)}   # a cliff above 5 rows
+    # 16 rows go as 4 blocks of 4 (4.0 against 6.0: a gain too)
+    assert cal.split_window_from_costs(cliff, 5) == {"min_q": 6, "max_q": 16, "min_kv": 4096, "max_chunk": 5}
+    # a width that does not gain ends the run
+    gap = {**cliff, 9: 1.5}
+    assert cal.split_window_from_costs(gap, 5) == {"min_q": 6, "max_q": 8, "min_kv": 4096, "max_chunk": 5}
+    assert cal._split_chunk({1: 1.0, 2: 1.2, 4: 1.6, 8: 8.0}) == 4     # lowest cost per row up to 8 rows
+
+
+def test_apply_sdpa_split_measures_once_and_obeys_enabled(cal, monkeypatch):
+    from dspark_rocm import sdpa_split
+
+    model = tiny_model("cpu", seed=6)
+    calls = []
+
+    def fake_costs(hq, hk, d, **kw):
+        calls.append((hq, hk, d))
+        return {q: (1.0 if q <= 4 else 5.0) for q in range(1, 17)}
+
+    monkeypatch.setattr(cal, "_stock_attention_costs", fake_costs)
+    cfg = cal.apply_sdpa_split(model, verbose=False)
+    a = model.args
+    assert calls == [(a.num_attention_heads, a.num_key_value_heads, a.head_dim)]
+    assert cfg == sdpa_split.SplitConfig(min_q=5, max_q=16, min_kv=4096, max_chunk=4) and cal.SDPA_SPLIT_CFG is cfg
+    assert cal.apply_sdpa_split(model, verbose=False) == cfg and len(calls) == 1      # cached
+    assert cal.apply_sdpa_split(model, enabled=False) is None and cal.SDPA_SPLIT_CFG is None
+    assert cal.apply_sdpa_split(model, enabled=True) == sdpa_split.SplitConfig()
+    assert cal.apply_sdpa_split(object(), verbose=False) == sdpa_split.SplitConfig()  # shape unreadable
+    monkeypatch.setattr(cal, "_stock_attention_costs", lambda *a, **k: {q: float(q) for q in range(1, 17)})
+    assert cal.measure_split_window(8, 2, 64, refresh=True, verbose=False) is None

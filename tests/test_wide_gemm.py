@@ -121,22 +121,15 @@ def test_widest_quantized_linear_picks_the_biggest_and_looks_through_model():
 
 
 def _fake_timing(monkeypatch, wins_from: int):
-    """Stock 2.0 ms vs wide 1.0 ms from ``wins_from`` rows, 1.0 vs 1.0 below it."""
-    import itertools
+    """The race on the widest weight: the wide path wins from ``wins_from`` rows."""
+    seen = []
 
-    state = {"rows": 0}
-    counter = itertools.count()
+    def fake_wins(lin, M, gen, exact, margin):
+        seen.append(M)
+        return M >= wins_from
 
-    def fake_probe(mod, M, gen):
-        state["rows"] = M
-        return torch.empty(0)
-
-    def fake_ms(fn, repeat=3):
-        stock = next(counter) % 2 == 0                       # stock timed first at each width
-        return 2.0 if stock and state["rows"] >= wins_from else 1.0
-
-    monkeypatch.setattr(wg, "_probe_x", fake_probe)
-    monkeypatch.setattr(wg, "_ms", fake_ms)
+    monkeypatch.setattr(wg, "_wide_wins", fake_wins)
+    return seen
 
 
 def test_crossover_never_returns_a_threshold_that_is_not_identical(monkeypatch):
@@ -144,7 +137,7 @@ def test_crossover_never_returns_a_threshold_that_is_not_identical(monkeypatch):
     the floor, so calibration refuses or moves wider to a width where it does verify."""
     model = torch.nn.Sequential(_lin(1024, K))
     _fake_timing(monkeypatch, wins_from=256)
-    monkeypatch.setattr(wg, "_matches", lambda mod, M, exact=True: M != wg.SAFE_MIN_ROWS)
+    monkeypatch.setattr(wg, "_agrees", lambda mod, M, exact=True: M != wg.SAFE_MIN_ROWS)
     assert wg.verified_shapes([model], wg.SAFE_MIN_ROWS, widths=()) == []
     got = wg.measure_crossover(model)
     assert got is None or (got[0] > wg.SAFE_MIN_ROWS and wg.verified_shapes([model], got[0], widths=()) == got[1])
@@ -152,10 +145,13 @@ def test_crossover_never_returns_a_threshold_that_is_not_identical(monkeypatch):
 
 def test_crossover_picks_the_first_width_that_keeps_winning(monkeypatch):
     model = torch.nn.Sequential(_lin(1024, K), _lin(512, K, bits=4))
-    _fake_timing(monkeypatch, wins_from=1024)
-    monkeypatch.setattr(wg, "_matches", lambda mod, M, exact=True: True)
-    got = wg.measure_crossover(model, widths=(256, 512, 1024, 2048))
+    seen = _fake_timing(monkeypatch, wins_from=1024)
+    monkeypatch.setattr(wg, "_agrees", lambda mod, M, exact=True: True)
+    got = wg.measure_crossover(model, widths=(128, 256, 512, 1024, 2048))
     assert got == (1024, [f"{K}x1024x8xbfloat16", f"{K}x512x4xbfloat16"])
+    assert seen == [256, 512, 1024, 2048]                      # under the floor: never raced
+    assert wg.gate.winning_tail([False, True, False, True, True]) == 3
+    assert wg.gate.winning_tail([True, True]) == 0 and wg.gate.winning_tail([True, False]) is None
     _fake_timing(monkeypatch, wins_from=10 ** 9)                # never faster: off
     assert wg.measure_crossover(model) is None
 
@@ -163,10 +159,10 @@ def test_crossover_picks_the_first_width_that_keeps_winning(monkeypatch):
 def test_verified_shapes_drops_a_shape_whose_kernel_raises(monkeypatch):
     model = torch.nn.Sequential(_lin(1024, K), _lin(512, K))
 
-    def matches(mod, M, exact=True):
+    def agrees(mod, M, exact=True):
         if int(mod.weight.shape[0]) == 512:
             raise RuntimeError("refused")
         return True
 
-    monkeypatch.setattr(wg, "_matches", matches)
+    monkeypatch.setattr(wg, "_agrees", agrees)
     assert wg.verified_shapes([model], 256) == [f"{K}x1024x8xbfloat16"]
