@@ -93,7 +93,7 @@ struct AttnArgs {
   const u16* vs;
   const u16* vb;
   const u32* anc;
-  float* opart;
+  float* opart;  // split-KV partials, fp32: o [B*Hk][NB][RP][D], m and l [B*Hk][NB][RP]
   float* mpart;
   float* lpart;
   u16* out;
@@ -227,8 +227,9 @@ constexpr float kOff4 = T::kF16 ? 0.0f : 128.0f;
 
 // Template parameters: T element type; D head dim (64, 128, 256); TREE ancestry mask; WV row
 // tiles per workgroup; KS waves splitting each tile's keys (1 or 2); PF tiles in flight (1 or
-// 2); QB quantized K/V field width (0 = plain T, 4 or 8).
-template <class T, int D, bool TREE, int WV, int KS, int PF, int QB>
+// 2); QB quantized K/V field width (0 = plain T, 4 or 8); PAD the caller's head dim is below D
+// (its missing columns of q, K and V are zeros that are never read, nor written out).
+template <class T, int D, bool TREE, int WV, int KS, int PF, int QB, bool PAD = false>
 __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(const AttnArgs a) {
   constexpr int DS = D == 256 ? 2 : 1;  // waves per row tile splitting the output columns
   constexpr int KT = D == 256 ? 32 : 64;  // keys per LDS tile
@@ -288,7 +289,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   // head dims below the instance's D: the missing columns of q, K and V are zeros (never read)
 #pragma unroll
   for (int c = 0; c < NDC; ++c)
-    qf[c] = 32 * c + 8 * q4 < a.dv ? ldg128(qrow + 32 * c + 8 * q4) : u32x4_t{0u, 0u, 0u, 0u};
+    qf[c] = (!PAD || 32 * c + 8 * q4 < a.dv) ? ldg128(qrow + 32 * c + 8 * q4) : u32x4_t{0u, 0u, 0u, 0u};
   if constexpr (QB == 4) {
     // 4-bit K fields sit in LDS in unpack4_off's order: q follows (its row sums do not change)
 #pragma unroll
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
   const int vkq = tid % VQ, vdc = tid / VQ;
   // a thread's K chunks all sit in column tid % DC (THREADS is a multiple of DC), its V chunks in
   // column vdc: columns at or past the head dim load nothing and stage zeros
-  const bool kcol = 8 * (tid % DC) < a.dv, vcol = 8 * vdc < a.dv;
+  const bool kcol = !PAD || 8 * (tid % DC) < a.dv, vcol = !PAD || 8 * vdc < a.dv;
   const u32x4_t zero4 = {0u, 0u, 0u, 0u};
   const u16* kbase16 = static_cast<const u16*>(a.k) + b * a.ksb + hk * a.ksh;
   const u16* vbase16 = static_cast<const u16*>(a.v) + b * a.vsb + hk * a.vsh;
@@ -724,7 +725,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
       u32x2_t pk2 = {pack2<T>(o[t][0] * inv, o[t][1] * inv), pack2<T>(o[t][2] * inv, o[t][3] * inv)};
-      if (dbase + 16 * t + 4 * q4 < a.dv) *reinterpret_cast<u32x2_t*>(orow + 16 * t + 4 * q4) = pk2;
+      if (!PAD || dbase + 16 * t + 4 * q4 < a.dv) *reinterpret_cast<u32x2_t*>(orow + 16 * t + 4 * q4) = pk2;
     }
     return;
   }
@@ -761,18 +762,19 @@ __global__ __launch_bounds__(256) void combine_kernel(const AttnArgs a) {
       const long pj = base + (long)j * a.RP;
       mj[i] = a.mpart[pj];
       lj[i] = a.lpart[pj];
+      const float* src = a.opart + pj * D + DPL * lane;
       if constexpr (DPL == 4) {
-        const float4 o4 = *reinterpret_cast<const float4*>(&a.opart[pj * D + 4 * lane]);
+        const float4 o4 = *reinterpret_cast<const float4*>(src);
         oj[i][0] = o4.x;
         oj[i][1] = o4.y;
         oj[i][2] = o4.z;
         oj[i][3] = o4.w;
       } else if constexpr (DPL == 2) {
-        const float2 o2 = *reinterpret_cast<const float2*>(&a.opart[pj * D + 2 * lane]);
+        const float2 o2 = *reinterpret_cast<const float2*>(src);
         oj[i][0] = o2.x;
         oj[i][1] = o2.y;
       } else {
-        oj[i][0] = a.opart[pj * D + lane];
+        oj[i][0] = *src;
       }
     }
     float mn = M;
@@ -830,12 +832,12 @@ DSPARK_ATTN_LAUNCH(F16, 64);
 DSPARK_ATTN_LAUNCH(F16, 128);
 DSPARK_ATTN_LAUNCH(F16, 256);
 
-template <class T, int D>
-int launch_impl(const AttnArgs& a, const Plan& p, long B, bool tree, int qbits, hipStream_t s) {
+template <class T, int D, bool PAD>
+void launch_p1(const AttnArgs& a, const Plan& p, long B, bool tree, int qbits, hipStream_t s) {
   const dim3 grid1((unsigned)(B * a.Hk), (unsigned)p.NB, (unsigned)p.NRG);
   constexpr int DS = D == 256 ? 2 : 1;
 #define DSPARK_P1(TR, W, K, F, Q) \
-  hipLaunchKernelGGL((p1_kernel<T, D, TR, W, K, F, Q>), grid1, dim3(64 * W * K * DS), 0, s, a)
+  hipLaunchKernelGGL((p1_kernel<T, D, TR, W, K, F, Q, PAD>), grid1, dim3(64 * W * K * DS), 0, s, a)
 #define DSPARK_P1_W(TR, Q)              \
   if (p.WV == 8) DSPARK_P1(TR, 8, 1, 2, Q); \
   else if (p.KS == 2) DSPARK_P1(TR, 4, 2, 1, Q); \
@@ -846,21 +848,28 @@ int launch_impl(const AttnArgs& a, const Plan& p, long B, bool tree, int qbits, 
     // the workspace is the plan's, with one more row group when there are more than 4 tiles)
     const dim3 grid4((unsigned)(B * a.Hk), (unsigned)p.NB, (unsigned)((a.RT + 3) / 4));
 #define DSPARK_P1_4(TR, Q) \
-  hipLaunchKernelGGL((p1_kernel<T, D, TR, 4, 1, 1, Q>), grid4, dim3(64 * 4 * DS), 0, s, a)
-    if (qbits == 8) DSPARK_P1_4(false, 8);
-    else if (qbits == 4) DSPARK_P1_4(false, 4);
+  hipLaunchKernelGGL((p1_kernel<T, D, TR, 4, 1, 1, Q, PAD>), grid4, dim3(64 * 4 * DS), 0, s, a)
+    if (!PAD && qbits == 8) DSPARK_P1_4(false, 8);
+    else if (!PAD && qbits == 4) DSPARK_P1_4(false, 4);
     else if (p.WV == 6) { if (tree) DSPARK_P1(true, 6, 1, 1, 0); else DSPARK_P1(false, 6, 1, 1, 0); }
     else if (tree) DSPARK_P1_4(true, 0);
     else DSPARK_P1_4(false, 0);
 #undef DSPARK_P1_4
   } else {
-    if (qbits == 8) { DSPARK_P1_W(false, 8) }
-    else if (qbits == 4) { DSPARK_P1_W(false, 4) }
+    if (!PAD && qbits == 8) { DSPARK_P1_W(false, 8) }
+    else if (!PAD && qbits == 4) { DSPARK_P1_W(false, 4) }
     else if (tree) { DSPARK_P1_W(true, 0) }
     else { DSPARK_P1_W(false, 0) }
   }
 #undef DSPARK_P1_W
 #undef DSPARK_P1
+}
+
+template <class T, int D>
+int launch_impl(const AttnArgs& a, const Plan& p, long B, bool tree, int qbits, hipStream_t s) {
+  // quantized caches hold whole groups of 64 along D: never padded (the entry point checks)
+  if (a.dv != D) launch_p1<T, D, true>(a, p, B, tree, 0, s);
+  else launch_p1<T, D, false>(a, p, B, tree, qbits, s);
   int st = check_launch("verify_attention(p1)");
   if (st || p.NB == 1) return st;
   hipLaunchKernelGGL((combine_kernel<T, D>), dim3((unsigned)(B * a.Hk * a.R)), dim3(256), 0, s, a);
