@@ -113,8 +113,8 @@ def test_verified_shapes_and_crossover_invariant(dev, monkeypatch):
     got = wg.measure_crossover(model)
     print("measured crossover:", got, flush=True)
     assert got is None or (got[0] >= wg.SAFE_MIN_ROWS and got[1] == keys)
-    real = wg._matches
-    monkeypatch.setattr(wg, "_matches", lambda mod, M, exact=True: M != wg.SAFE_MIN_ROWS and real(mod, M, exact))
+    real = wg._agrees
+    monkeypatch.setattr(wg, "_agrees", lambda mod, M, exact=True: M != wg.SAFE_MIN_ROWS and real(mod, M, exact))
     assert wg.verified_shapes([model], wg.SAFE_MIN_ROWS, widths=()) == []
     got = wg.measure_crossover(model)
     assert got is None or (got[0] > wg.SAFE_MIN_ROWS and wg.verified_shapes([model], got[0], widths=()) == got[1])
