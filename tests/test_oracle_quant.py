@@ -93,3 +93,33 @@ def test_torch_quant_matches_oracle():
         deq = quant.dequantize(pw, s, b, bits=bits)
         assert float((deq - w).abs().max()) <= float(s.float().max()) * 0.5 + 1e-3
     assert "dspark_rocm" in sys.modules
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantize_rule_kats(bits):
+    """The quantizer's rule at its fixed points: bias = bf16(min), scale = bf16((max - min) /
+    (2^bits - 1)); the group minimum maps to field 0, the maximum to round((max - min) / scale)
+    (the top field unless the scale's bf16 rounding went up); a constant group has scale 0
+    (fields 0, bias = the value); a midpoint rounds half to even."""
+    levels = (1 << bits) - 1
+    w = np.zeros((3, 64), np.float32)
+    w[0] = np.linspace(-1.0, 2.0, 64, dtype=np.float32)
+    w[1] = 0.75
+    w[2, :32], w[2, 32:] = -0.5, 0.5
+    q, s, b = quant_ref.quantize(w, bits)
+    f = quant_ref.unpack(q, bits)
+    assert b[0, 0] == -1.0 and s[0, 0] == quant_ref.bf16_round(np.float32(3.0 / levels))
+    assert f[0, 0] == 0 and f[0, -1] == levels
+    assert s[1, 0] == 0.0 and b[1, 0] == 0.75 and not f[1].any()
+    # range 1.0: scale = bf16(1/levels) rounds up (1/255 -> 0x3B81 = 0.0039367676, 1/15 ->
+    # 0x3D89 = 0.0668945), so the top value lands at round(1 / scale): 254 at 8 bits, 15 at 4
+    top = {8: 254, 4: 15}[bits]
+    assert s[2, 0] == {8: 0.003936767578125, 4: 0.06689453125}[bits]
+    assert b[2, 0] == -0.5 and set(f[2].tolist()) == {0, top}
+    # a value exactly halfway between two fields takes the even one
+    half = np.zeros((1, 64), np.float32)
+    half[0, 1] = 1.0                         # scale 1/levels, bias 0
+    sc = float(quant_ref.quantize(half, bits)[1][0, 0])
+    half[0, 2] = np.float32(2.5 * sc)        # 2.5 steps above the bias
+    f2 = quant_ref.unpack(quant_ref.quantize(half, bits)[0], bits)
+    assert f2[0, 2] == 2
