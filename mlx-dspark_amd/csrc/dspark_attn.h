@@ -127,13 +127,17 @@ inline Plan make_plan(long B, long Hq, long Hk, long Mq, long D, long L) {
   p.NRG = (p.RT + p.WV - 1) / p.WV;
   // Long caches: ~2 workgroups of 4 waves per CU (256 CUs), or one of 8 waves (twice the
   // rows per K/V tile: the fp32 partials, written here and read by the combine, double too),
-  // which then keeps two tiles in flight. At least 256 keys per block. When that caps the
-  // blocks below one workgroup per CU, 4-row-tile heads of head dim <= 128 split each tile's
-  // keys over 8 waves. Row groups beyond one re-read the head's K/V.
+  // which then keeps two tiles in flight. At least 256 keys per block from 4096 keys on; a
+  // shorter cache, whose blocks that floor caps well below one workgroup per CU, takes blocks
+  // of 128 keys (64 up to 1280): its time is a few tiles' latency per block, which shorter
+  // blocks cut by more than the extra partials cost. When the blocks still stay below one
+  // workgroup per CU, 4-row-tile heads of head dim <= 128 split each tile's keys over 8
+  // waves. Row groups beyond one re-read the head's K/V.
   const long heads = B * Hk * p.NRG;
   const long target = (p.WV == 8 || D == 256) ? 256 : 512;
   long nb = (target + heads - 1) / heads;
-  const long max_nb = (L + 255) / 256;
+  const long min_keys = L <= 1280 ? 64 : (L < 4096 ? 128 : 256);
+  const long max_nb = (L + min_keys - 1) / min_keys;
   if (nb > max_nb) nb = max_nb;
   if (nb < 1) nb = 1;
   if (p.WV == 4 && D <= 128 && heads * nb < 256) p.KS = 2;
