@@ -579,8 +579,7 @@ __global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(c
 #pragma unroll
         for (int i = 0; i < 4; ++i) smax = fmaxf(smax, s[ks][i]);
     }
-    smax = fmaxf(smax, shfl_xor(smax, 16));
-    smax = fmaxf(smax, shfl_xor(smax, 32));
+    smax = max_xor32(max_xor16(smax));
     const float mn = fmaxf(m, smax * a.scale_log2);
     const float alpha = exp2_raw(m - mn);
     m = mn;

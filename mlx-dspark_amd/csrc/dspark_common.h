@@ -71,6 +71,25 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
       float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
 }
 
+// max(v, v of lane l ^ 16) and max(v, v of lane l ^ 32) in every lane, with the gfx950 row
+// swaps (v_permlane16_swap: rows 0 <-> 1 and 2 <-> 3 of 16 lanes; v_permlane32_swap: the two
+// 32-lane halves) on two copies of v: after the swap each lane holds its own value in one
+// register and its partner's in the other, in an order that depends on the lane, which a
+// commutative max does not see (the same bits as a ds_bpermute exchange, without its LDS
+// round trip). Inline asm: given the same value twice, the builtins' two results are folded
+// into one by the compiler (they differ: the swap moves rows). s_nop 1 covers the wait states
+// between a VALU write of either register and the swap reading it.
+__device__ __forceinline__ float max_xor16(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(a, b);
+}
+
 // Sum over each aligned group of 8 lanes, returned to all 8: the butterfly over lane bits 0,
 // 1, 2 (v + v^1, then + v^2, then + v^4) with DPP exchanges (quad permutes, half-row mirror:
 // lane i of an 8-lane group pairs with 7 - i, which holds the other quad's sum).
