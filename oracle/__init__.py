@@ -1,7 +1,7 @@
 """CPU oracle for the speculative-verify hot path — TEST INFRASTRUCTURE, not product code.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import
-anything from this package, and only as the checker (or the timed CPU baseline). The product
+anything from this package, and only to check results (or as the timed CPU baseline). The product
 path (``mlx-dspark_amd``) never imports it.
 
 What it restates (ARahim3/mlx-dspark v0.20.4, ``src/mlx_dspark/`` unless noted):
