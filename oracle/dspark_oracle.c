@@ -1,6 +1,6 @@
 /*
  * dspark_oracle.c — C (OpenMP) restatement of the verify hot path. TEST INFRASTRUCTURE ONLY:
- * used by tests/ as a checker for large shapes and by bench.py as the timed CPU baseline.
+ * used by tests/ to check large shapes and by bench.py as the timed CPU baseline.
  * Never linked into the product library.
  *
  *  orc_qmm        factored affine qmm (skinny_qmm.py:86-158; A.1): per group g,
