@@ -13,9 +13,10 @@
 //     to 4 or 8 row tiles of 16 rows (all gqa*Mq rows of the head when there are at most 128),
 //     so each K/V byte is read from HBM once and shared by every query head of the GQA group.
 //     On short caches (few blocks) the 4 row tiles are worked by 8 waves, two per tile
-//     splitting its keys. Head dim 256 gives each row tile two waves, one per half of the
-//     output columns; both compute the whole score tile (no exchange), and tiles are 32 keys
-//     so two K/V buffers still fit in LDS.
+//     splitting its keys. Head dim 256 takes 32-key tiles so two K/V buffers still fit in
+//     LDS, one wave per row tile over all 256 output columns with two tiles in flight (a
+//     quantized cache: two waves per row tile, one per half of the output columns, both
+//     computing the whole score tile, one tile in flight: its registers do not fit one wave).
 //   * key tiles are staged through two alternating LDS buffers (one barrier per tile) from
 //     registers loaded one (4-wave workgroups) or two (8-wave workgroups) tiles ahead: K
 //     row-major (padded rows), V transposed (key-contiguous, 8-key blocks XOR-swizzled by d)
@@ -119,8 +120,8 @@ inline Plan make_plan(long B, long Hq, long Hk, long Mq, long D, long L) {
   p.R = (int)((Hq / Hk) * Mq);
   p.RT = (p.R + 15) / 16;
   p.RP = p.RT * 16;
-  // head dim 256 runs two waves per row tile: up to 6 row tiles (12 waves of <= 168 VGPRs,
-  // three per SIMD), so a 24/4-head group's 96 rows share one pass over K/V
+  // head dim 256: up to 6 row tiles of one wave each (two waves per SIMD), so a 24/4-head
+  // group's 96 rows share one pass over K/V
   p.WV = p.RT > 4 ? (D <= 128 ? 8 : 6) : 4;
   p.KS = 1;
   p.PF = p.WV == 8 ? 2 : 1;
@@ -232,10 +233,11 @@ constexpr float kOff4 = T::kF16 ? 0.0f : 128.0f;
 // Template parameters: T element type; D head dim (64, 128, 256); TREE ancestry mask; WV row
 // tiles per workgroup; KS waves splitting each tile's keys (1 or 2); PF tiles in flight (1 or
 // 2); QB quantized K/V field width (0 = plain T, 4 or 8); PAD the caller's head dim is below D
-// (its missing columns of q, K and V are zeros that are never read, nor written out).
-template <class T, int D, bool TREE, int WV, int KS, int PF, int QB, bool PAD = false>
-__global__ __launch_bounds__(64 * WV * KS * (D == 256 ? 2 : 1)) void p1_kernel(const AttnArgs a) {
-  constexpr int DS = D == 256 ? 2 : 1;  // waves per row tile splitting the output columns
+// (its missing columns of q, K and V are zeros that are never read, nor written out); DSX waves
+// per row tile, each taking D / DSX of the output columns (2 only for quantized head dim 256).
+template <class T, int D, bool TREE, int WV, int KS, int PF, int QB, bool PAD = false, int DSX = (D == 256 ? 2 : 1)>
+__global__ __launch_bounds__(64 * WV * KS * DSX) void p1_kernel(const AttnArgs a) {
+  constexpr int DS = DSX;  // waves per row tile splitting the output columns
   constexpr int KT = D == 256 ? 32 : 64;  // keys per LDS tile
   static_assert(KS == 1 || KS == 2, "key split");
   static_assert(PF == 1 || PF == 2, "tiles in flight");
@@ -846,17 +848,22 @@ void launch_p1(const AttnArgs& a, const Plan& p, long B, bool tree, int qbits, h
   else if (p.KS == 2) DSPARK_P1(TR, 4, 2, 1, Q); \
   else DSPARK_P1(TR, 4, 1, 1, Q);
   if constexpr (D == 256) {
-    // two waves per row tile, no key split; 4 or 6 row tiles (quantized K/V: always 4, whose
-    // registers do not fit three waves per SIMD; the same key blocks and partial layout, so
-    // the workspace is the plan's, with one more row group when there are more than 4 tiles)
+    // plain K/V: one wave per row tile over all 256 columns, two tiles in flight, 4 or 6 row
+    // tiles. Quantized K/V: two waves per row tile, one per half of the columns (a wave's
+    // registers do not hold all 256), always 4 row tiles; the same key blocks and partial
+    // layout, so the workspace is the plan's, with one more row group when there are more
+    // than 4 tiles.
     const dim3 grid4((unsigned)(B * a.Hk), (unsigned)p.NB, (unsigned)((a.RT + 3) / 4));
 #define DSPARK_P1_4(TR, Q) \
   hipLaunchKernelGGL((p1_kernel<T, D, TR, 4, 1, 1, Q, PAD>), grid4, dim3(64 * 4 * DS), 0, s, a)
+#define DSPARK_P1_S(TR, W, G) \
+  hipLaunchKernelGGL((p1_kernel<T, D, TR, W, 1, 2, 0, PAD, 1>), G, dim3(64 * W), 0, s, a)
     if (!PAD && qbits == 8) DSPARK_P1_4(false, 8);
     else if (!PAD && qbits == 4) DSPARK_P1_4(false, 4);
-    else if (p.WV == 6) { if (tree) DSPARK_P1(true, 6, 1, 1, 0); else DSPARK_P1(false, 6, 1, 1, 0); }
-    else if (tree) DSPARK_P1_4(true, 0);
-    else DSPARK_P1_4(false, 0);
+    else if (p.WV == 6) { if (tree) DSPARK_P1_S(true, 6, grid1); else DSPARK_P1_S(false, 6, grid1); }
+    else if (tree) DSPARK_P1_S(true, 4, grid4);
+    else DSPARK_P1_S(false, 4, grid4);
+#undef DSPARK_P1_S
 #undef DSPARK_P1_4
   } else {
     if (!PAD && qbits == 8) { DSPARK_P1_W(false, 8) }
