@@ -167,10 +167,14 @@ __device__ __forceinline__ int vt_pos(int key) {
 __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // swizzled element offset of (d, pos) in the transposed V tile (row pitch KT): the 8-key block
-// index is XORed with bits of d, a permutation of each row's blocks
+// index is XORed with bits of d, a permutation of each row's blocks. The bits are the ones an
+// LDS conflict probe found to keep both the staging stores and the P.V fragment reads free of
+// bank conflicts: d >> 1 and d >> 3 for 64-key tiles, d >> 1 alone for 32-key tiles (with
+// d >> 3 too, every 32-key fragment read took a 2-way conflict).
 template <int KT>
 __device__ __forceinline__ int vt_off(int d, int pos) {
-  return d * KT + ((((pos >> 3) ^ (d >> 1) ^ (d >> 3)) & (KT / 8 - 1)) << 3) + (pos & 7);
+  const int sw = KT == 64 ? ((d >> 1) ^ (d >> 3)) : (d >> 1);
+  return d * KT + ((((pos >> 3) ^ sw) & (KT / 8 - 1)) << 3) + (pos & 7);
 }
 
 // 8 integer fields as 8 T values (exact: at most 255)
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(64 * WV * KS * DSX) void p1_kernel(const AttnArgs a
   constexpr int NU = KT / 32 / KS;    // 32-key halves of a tile per wave (P.V MFMA k-steps)
   static_assert(NU >= 1, "tile split");
   constexpr int DH = D / DS;          // output columns per wave
-  constexpr int KP = D + 8;           // padded K row (elements)
+  constexpr int KP = D + 16;          // padded K row (elements): 32 bytes keep the score reads conflict-free
   constexpr int DC = D / 8;           // 16-byte chunks of a T row
   constexpr int LOADS = (KT * DC + THREADS - 1) / THREADS;  // 16-byte K chunks per thread per tile (plain)
   constexpr bool KPART = LOADS * THREADS != KT * DC;       // the last round covers part of the threads
