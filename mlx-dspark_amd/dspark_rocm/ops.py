@@ -93,9 +93,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
 def quantized_matmul_multi(x_list, w_list, s_list, b_list, *, group_size: int = GROUP, bits: int = 4,
                            outs=None, workspace: torch.Tensor | None = None) -> list[torch.Tensor]:
     """Several ``quantized_matmul`` with the same M, K and bits in ONE launch (q/k/v; gate/up).
-    Bitwise equal to separate calls, except that an 8-bit [4096, 4096] matrix (which alone takes
-    the whole-K kernel) may differ by an fp32 rounding of a bias term when one group of 64 x
-    values spans many binades (its per-group sums of x are then not exact in fp32)."""
+    The K slice count of a launch depends on the strips of all its problems, so a matrix gives
+    the bits of a separate call whenever the launch keeps its slice count (the usual case; a
+    different count reassociates the fp32 slice partials, within the qmm tolerance). An 8-bit
+    [4096, 4096] matrix alone takes the whole-K kernel, which may also differ by an fp32 rounding
+    of a bias term when one group of 64 x values spans many binades."""
     cnt = len(w_list)
     if not 1 <= cnt <= _lib.MAX_QMM_PROBLEMS:
         raise ValueError(f"1..{_lib.MAX_QMM_PROBLEMS} problems per launch, got {cnt}")
