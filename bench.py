@@ -99,6 +99,23 @@ def _median_replay_ms(g, repeats: int = REPEATS) -> float:
     return statistics.median(times)
 
 
+def gate_up_kernel_name(ls) -> str:
+    """The kernel the layer set's gate+up launch runs (the library's plan query), with its grid."""
+    from dspark_rocm import ops
+
+    P = ls.packs[0]
+    p = ops.packed_multi_plan([ls.x["gu"]], [P["gate"], P["up"]])
+    k = P["gate"].k
+    if p["kernel"] == "whole-K per CU":
+        name = f"qmm_cu_kernel<{ls.bits},{p['tiles_per_workgroup']},{k // 64 // p['slices']}>"
+    elif p["kernel"] == "whole-K tile":
+        name = f"qmm_wk_kernel<{ls.bits},8,true,true>"
+    else:
+        name = f"qmm_sk_kernel<{ls.bits},4,{16 if k // 64 // p['slices'] > 8 else 8},true,true,false>"
+    return (f"{name} gate+up launch, packed form (N=2x{P['gate'].n}, K={k}, M={ls.m}; "
+            f"{p['workgroups']} workgroups, {p['kernel']})")
+
+
 def time_graph(fn, repeats: int = REPEATS, warm: int = 2):
     """Capture ``fn`` (which enqueues work on the current stream) into a HIP graph on a warmed
     side stream; returns (median ms per replay over ``repeats`` event-bracketed replays, graph)."""
@@ -728,6 +745,7 @@ def main() -> None:
     gbs = ls.bytes_per_step / (ms_step * 1e-3) / 1e9
     log(f"layer-set graph: {ms_step * 1e3:.2f} us/step, {gbs:.1f} GB/s (median of {REPEATS} replays)")
 
+    log(f"gate/up kernel: {gate_up_kernel_name(ls)}")
     # dominant kernel: K gate/up launches back to back (rotating layers) as one graph, HIP events
     # on the launch stream around each replay; average launch = replay / K
     gu_total, _ = time_graph(lambda: [ls.gate_up(i) for i in range(K)])
@@ -737,8 +755,7 @@ def main() -> None:
                                ls.gu_flops)}
     gu = legs["qmm_gate_up"]
     log(f"gate/up launch: {gu_us:.2f} us, {gu['GBs']} GB/s")
-    roofline = {"kernel": "qmm_sk_kernel<8,4,16,true,true,false> gate+up launch, packed form (N=2x12288, K=4096, "
-                          "M=16; grid 384x4)", "bound": "hbm", "achieved": gu["GBs"], "peak": HBM_PEAK_GBS,
+    roofline = {"kernel": gate_up_kernel_name(ls), "bound": "hbm", "achieved": gu["GBs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": gu["frac"], "traffic": (traffic or {}).get("qmm_gate_up_bytes"),
                 "bytes_per_launch": ls.gu_bytes, "avg_launch_us": gu["us"], "frac_of_measured": gu["frac_of_measured"],
                 "mfma_util": gu["mfma_util"]}

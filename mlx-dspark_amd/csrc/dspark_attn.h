@@ -220,7 +220,7 @@ __device__ __forceinline__ void fields8(const u32* w, int first, u32* out) {
 template <class T>
 __device__ __forceinline__ u32x4_t unpack4_off(u32 w) {
   if constexpr (T::kF16) {
-    const u32 m = 0x000F000Fu, c = 0x64006400u;
+    const u32 m = opaque_sgpr(0x000F000Fu), c = opaque_vgpr(0x64006400u);
     const f16x2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
     auto pair = [&](u32 x) { return __builtin_bit_cast(u32, __builtin_bit_cast(f16x2_t, and_or(x, m, c)) - off); };
     return u32x4_t{pair(w), pair(w >> 4), pair(w >> 8), pair(w >> 12)};

@@ -104,12 +104,24 @@ __device__ __forceinline__ float sum8_lanes(float v) {
   return v;
 }
 
-// (v & m) | o as one v_and_or_b32 (the mask in an SGPR, o in a VGPR): the compiler splits it
-// into two instructions when both constants are literals.
-__device__ __forceinline__ u32 and_or(u32 v, u32 m, u32 o) {
-  u32 d;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(v), "s"(m), "v"(o));
-  return d;
+// (v & m) | o. Written in C, not as inline asm, so the compiler sees the VALU write: an MFMA
+// that reads the result needs two wait states after it, which the compiler inserts only for
+// instructions it can see (an inline-asm v_and_or_b32 feeding the unpacked weights to an MFMA
+// one instruction later gave wrong products in some schedules). It selects one v_and_or_b32
+// when m sits in an SGPR and o in a VGPR (opaque_sgpr / opaque_vgpr); with both as literals it
+// would emit a v_and and a v_or.
+__device__ __forceinline__ u32 and_or(u32 v, u32 m, u32 o) { return (v & m) | o; }
+
+// A constant the compiler must keep in a scalar / vector register instead of folding it into
+// the instructions that use it (an empty asm: no instruction, so nothing is hidden from the
+// hazard tracking; identical ones are shared).
+__device__ __forceinline__ u32 opaque_sgpr(u32 v) {
+  asm("" : "+s"(v));
+  return v;
+}
+__device__ __forceinline__ u32 opaque_vgpr(u32 v) {
+  asm("" : "+v"(v));
+  return v;
 }
 
 // Wave-uniform copy of a value the compiler cannot prove uniform (e.g. threadIdx.x >> 6).

@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <mutex>
 
+#include "dspark_qmm_cu.h"
 #include "dspark_qmm_splitk.h"
 #include "dspark_qmm_wholek.h"
 
@@ -132,6 +133,52 @@ int launch_wk(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
   hipLaunchKernelGGL((qmm_wk_kernel<8, kWkWaves, PACKED, SBVEC>), dim3(p.tiles, p.mtiles), dim3(64 * kWkWaves), 0, st,
                      a);
   return check_launch(PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
+}
+
+// One workgroup per CU over all of K (dspark_qmm_cu.h): packed weights, K = 4096, one x for
+// every problem, and 3..6 tiles per CU filling at least 240 CUs; the slices of the split-K
+// plan (8 or 16 groups) fix the association, so the bits are that plan's. Returns the tiles
+// per workgroup, or 0 when the launch takes the split-K kernel.
+int cu_tpw(const dspark_qmm_problem* problems, int count, const long* Ns, long K, const Plan& p) {
+  if (K != kCuK || p.wholek || p.S < 2 || (K / 64) % p.S || ((K / 64) / p.S != 8 && (K / 64) / p.S != 16)) return 0;
+  long tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    if (problems[i].x != problems[0].x || problems[i].ldx != problems[0].ldx) return 0;
+    tiles += (Ns[i] + 15) / 16;
+  }
+  const long tpw = (tiles + kCUs - 1) / kCUs;
+  if (tpw < 3 || tpw > 6 || (tiles + tpw - 1) / tpw < 240) return 0;
+  return (int)tpw;
+}
+
+template <int BITS, int TPW, int GSL>
+int launch_cu_t(const QmmSkArgs& a, const Plan& p, int tiles, hipStream_t st) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_cu_kernel<BITS, TPW, GSL>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)cu_lds_bytes(TPW));
+  });
+  if (attr != hipSuccess) return fail(DSPARK_ERR_LAUNCH, "dspark_qmm_packed: LDS attribute: %s", hipGetErrorString(attr));
+  hipLaunchKernelGGL((qmm_cu_kernel<BITS, TPW, GSL>), dim3((unsigned)((tiles + TPW - 1) / TPW), p.mtiles),
+                     dim3(128 * TPW), cu_lds_bytes(TPW), st, a, tiles);
+  return check_launch("dspark_qmm_packed");
+}
+
+template <int BITS, int GSL>
+int launch_cu_g(const QmmSkArgs& a, const Plan& p, int tpw, int tiles, hipStream_t st) {
+  switch (tpw) {
+    case 3: return launch_cu_t<BITS, 3, GSL>(a, p, tiles, st);
+    case 4: return launch_cu_t<BITS, 4, GSL>(a, p, tiles, st);
+    case 5: return launch_cu_t<BITS, 5, GSL>(a, p, tiles, st);
+    default: return launch_cu_t<BITS, 6, GSL>(a, p, tiles, st);
+  }
+}
+
+int launch_cu(const QmmSkArgs& a, const Plan& p, int bits, long G, int tpw, int tiles, hipStream_t st) {
+  const bool g16 = G / p.S == 16;
+  if (bits == 8) return g16 ? launch_cu_g<8, 16>(a, p, tpw, tiles, st) : launch_cu_g<8, 8>(a, p, tpw, tiles, st);
+  return g16 ? launch_cu_g<4, 16>(a, p, tpw, tiles, st) : launch_cu_g<4, 8>(a, p, tpw, tiles, st);
 }
 
 template <int BITS, bool SWIGLU = false>
@@ -353,7 +400,17 @@ int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bit
     if (packed) return launch_wk<true, true>(a, p, s);
     return sbvec ? launch_wk<false, true>(a, p, s) : launch_wk<false, false>(a, p, s);
   }
-  if (packed) return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
+  if (packed) {
+    if (const int tpw = cu_tpw(problems, count, Ns, K, p)) {  // blockIdx.x counts TPW-tile groups
+      int t0 = 0;
+      for (int i = 0; i < count; ++i) {
+        a.p[i].strip0 = t0;
+        t0 += (int)((problems[i].N + 15) / 16);
+      }
+      return launch_cu(a, p, bits, G, tpw, t0, s);
+    }
+    return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
+  }
   return bits == 4 ? launch_bits<4>(a, p, sbvec, s) : launch_bits<8>(a, p, sbvec, s);
 }
 
@@ -545,6 +602,25 @@ extern "C" int dspark_qmm_packed_multi(const dspark_qmm_packed_problem* problems
   if (st) return st;
   return multi_impl(views, count, M, bits, group_size, true, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dspark_qmm_packed_multi_plan(const dspark_qmm_packed_problem* problems, int count, int64_t M, int bits,
+                                            int group_size, int32_t* out) {
+  if (!out) return fail(DSPARK_ERR_ARG, "qmm_plan: null output");
+  dspark_qmm_problem views[kQmmMaxProblems];
+  long Ns[kQmmMaxProblems];
+  int st = packed_views(problems, count, bits, views);
+  if (st || (st = validate(views, count, M, bits, group_size, Ns, true))) return st;
+  const Plan p = make_plan(Ns, count, views[0].K, M, bits, true);
+  if (p.S == 0) return fail(DSPARK_ERR_SHAPE, "qmm_plan: shape refused");
+  const int tpw = cu_tpw(views, count, Ns, views[0].K, p);
+  long tiles = 0;
+  for (int i = 0; i < count; ++i) tiles += (Ns[i] + 15) / 16;
+  out[0] = p.wholek ? 1 : tpw ? 2 : 0;
+  out[1] = p.S;
+  out[2] = tpw;
+  out[3] = p.wholek ? p.tiles * p.mtiles : tpw ? (int)((tiles + tpw - 1) / tpw) * p.mtiles : p.S * p.strips * p.mtiles;
+  return DSPARK_OK;
 }
 
 extern "C" size_t dspark_qmm_packed_multi_workspace(const dspark_qmm_packed_problem* problems, int count, int64_t M,

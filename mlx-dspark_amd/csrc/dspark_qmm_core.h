@@ -9,7 +9,7 @@ namespace dspark {
 
 // bf16 pair (128 + nibble t, 128 + nibble t+4) of a packed 4-bit word, for t = 0..3.
 __device__ __forceinline__ u32x4_t unpack_u4(u32 w) {
-  const u32 m = 0x000F000Fu, c = 0x43004300u;
+  const u32 m = opaque_sgpr(0x000F000Fu), c = opaque_vgpr(0x43004300u);
   return u32x4_t{and_or(w, m, c), and_or(w >> 4, m, c), and_or(w >> 8, m, c), and_or(w >> 12, m, c)};
 }
 

@@ -105,6 +105,8 @@ SIGNATURES: dict[str, tuple] = {
                                         c_size_t, c_void_p]),
     "dspark_qmm_packed_multi_workspace": (c_size_t, [ctypes.POINTER(QmmPackedProblem), c_int, c_i64, c_int,
                                                      c_int]),
+    "dspark_qmm_packed_multi_plan": (c_int, [ctypes.POINTER(QmmPackedProblem), c_int, c_i64, c_int, c_int,
+                                             ctypes.POINTER(ctypes.c_int32)]),
     "dspark_qmm_swiglu_packed_bytes": (c_size_t, [c_i64, c_i64, c_int, c_int]),
     "dspark_qmm_pack_swiglu": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_i64,
                                        c_int, c_int, c_void_p, c_size_t, c_void_p]),

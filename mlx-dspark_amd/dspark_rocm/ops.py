@@ -168,9 +168,10 @@ def qmm_pack(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, bit
     return PackedQmm(buf, n, k, bits)
 
 
-def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROUP, outs=None,
-                                  workspace: torch.Tensor | None = None) -> list[torch.Tensor]:
-    """``quantized_matmul_multi`` over packed matrices (one launch, same M, K and bits)."""
+def _packed_problems(x_list, packed_list, outs):
+    """(problems, count, M, bits, results, keep-alive list) of a packed multi launch. One x
+    tensor given for several problems stays one x (one copy when it must be made contiguous),
+    which the one-workgroup-per-CU kernel requires."""
     cnt = len(packed_list)
     if not 1 <= cnt <= _lib.MAX_QMM_PROBLEMS:
         raise ValueError(f"1..{_lib.MAX_QMM_PROBLEMS} problems per launch, got {cnt}")
@@ -178,7 +179,7 @@ def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROU
         x_list = list(x_list) * cnt
     bits = packed_list[0].bits
     probs = (_lib.QmmPackedProblem * cnt)()
-    results, keep, m = [], [], None
+    results, keep, m, rows = [], [], None, {}
     for i in range(cnt):
         x, pq = x_list[i], packed_list[i]
         _require_cuda(x, pq.buf)
@@ -188,17 +189,41 @@ def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROU
         k = x.shape[-1]
         if k != pq.k:
             raise ValueError(f"x has K={k}, the packed matrix K={pq.k}")
-        x2 = x.reshape(-1, k)
-        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-            x2 = x2.contiguous()
+        x2 = rows.get(id(x))
+        if x2 is None:
+            x2 = x.reshape(-1, k)
+            if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+                x2 = x2.contiguous()
+            rows[id(x)] = x2
         if m is None:
             m = x2.shape[0]
         elif x2.shape[0] != m:
             raise ValueError("all problems must have the same number of rows")
         y = outs[i] if outs is not None else torch.empty((m, pq.n), dtype=torch.bfloat16, device=x.device)
-        keep += [x2, y]
+        keep += [x, x2, y]
         probs[i] = _lib.QmmPackedProblem(_ptr(x2), x2.stride(0), _ptr(pq.buf), _ptr(y), y.stride(0), pq.n, k)
         results.append(y.reshape(*x.shape[:-1], pq.n))
+    return probs, cnt, m, bits, results, keep
+
+
+PACKED_KERNELS = ("split-K", "whole-K tile", "whole-K per CU")
+
+
+def packed_multi_plan(x_list, packed_list, *, group_size: int = GROUP) -> dict:
+    """The kernel ``quantized_matmul_packed_multi`` runs for these operands (host-only query):
+    ``kernel`` (one of ``PACKED_KERNELS``), ``slices`` (the split-K association the bits
+    follow), ``tiles_per_workgroup`` (per-CU kernel) and ``workgroups``."""
+    probs, cnt, m, bits, _, keep = _packed_problems(x_list, packed_list, None)
+    out = (ctypes.c_int32 * 4)()
+    _lib.call("dspark_qmm_packed_multi_plan", probs, cnt, m, bits, group_size, out)
+    return {"kernel": PACKED_KERNELS[out[0]], "slices": out[1], "tiles_per_workgroup": out[2],
+            "workgroups": out[3]}
+
+
+def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROUP, outs=None,
+                                  workspace: torch.Tensor | None = None) -> list[torch.Tensor]:
+    """``quantized_matmul_multi`` over packed matrices (one launch, same M, K and bits)."""
+    probs, cnt, m, bits, results, keep = _packed_problems(x_list, packed_list, outs)
     nbytes = _lib.load().dspark_qmm_packed_multi_workspace(probs, cnt, m, bits, group_size)
     ws = _pick(workspace, x_list[0].device, nbytes, qmm=True)
     _lib.call("dspark_qmm_packed_multi", probs, cnt, m, bits, group_size, _ptr(ws),

@@ -111,6 +111,58 @@ def test_multi_equals_single(dev):
         assert torch.equal(y, ops.quantized_matmul(x, wd, sd, bd, bits=bits))
 
 
+# K = 4096 launches of 3..6 row tiles per CU take the one-workgroup-per-CU kernel: 768, 1024,
+# 1216 (the last workgroup one tile) and 1531 tiles (two problems, the first ending in a half
+# tile inside a workgroup that holds the second's first tiles). Its bits are the split-K
+# kernel's for the same launch (the reference-layout multi launch: the slice count depends on
+# every problem's strips) at every M, and rows of both ends of N are held to the oracle.
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("ns", [(12288,), (16384,), (19456,), (12200, 12288)])
+def test_per_cu_kernel_bit_identical_to_split_k(dev, bits, ns):
+    import torch
+
+    from dspark_rocm import ops
+
+    k = 4096
+    mats = [_quantized(11 * i + bits, n, k, bits) for i, n in enumerate(ns)]
+    devs = [_dev(*m, dev) for m in mats]
+    packs = [ops.qmm_pack(*d, bits=bits) for d in devs]
+    for m in (1, 16, 33):
+        x = randn_bf16(rng(m + sum(ns)), m, k)
+        wide = torch.zeros((m, k + 64), dtype=torch.bfloat16, device=dev)
+        wide[:, 32:32 + k] = to_dev_bf16(x, dev)
+        for xd in (to_dev_bf16(x, dev), wide[:, 32:32 + k]):   # contiguous rows, then ldx = K + 64
+            plan = ops.packed_multi_plan([xd], packs)
+            tiles = sum((n + 15) // 16 for n in ns)
+            assert plan["kernel"] == "whole-K per CU", plan
+            assert plan["tiles_per_workgroup"] == -(-tiles // 256)
+            got = ops.quantized_matmul_packed_multi([xd], packs)
+            want = ops.quantized_matmul_multi([xd], [d[0] for d in devs], [d[1] for d in devs],
+                                              [d[2] for d in devs], bits=bits)
+            for y, w in zip(got, want):
+                assert torch.equal(y, w), (ns, m)
+        if m == 16:
+            for (wq, s, b), y in zip(mats, got):
+                yh = from_dev_bf16(y)
+                for sl in (slice(0, 128), slice(wq.shape[0] - 136, wq.shape[0])):
+                    want = qmm_ref.qmm_f64(x, wq[sl], s[sl], b[sl], bits)
+                    assert_rms_close(yh[:, sl], want, 2e-2, f"per-CU {bits}-bit {ns} rows {sl}")
+
+
+def test_per_cu_kernel_needs_one_x(dev):
+    """Problems reading different x tensors, or a launch of too few tiles, keep the split-K
+    kernel."""
+    from dspark_rocm import ops
+
+    k, bits = 4096, 8
+    packs = [ops.qmm_pack(*_dev(*_quantized(40 + i, 12288, k, bits), dev), bits=bits) for i in range(2)]
+    x = to_dev_bf16(randn_bf16(rng(5), 16, k), dev)
+    assert ops.packed_multi_plan([x], packs)["kernel"] == "whole-K per CU"
+    assert ops.packed_multi_plan([x, x.clone()], packs)["kernel"] == "split-K"
+    small = ops.qmm_pack(*_dev(*_quantized(3, 1024, k, bits), dev), bits=bits)
+    assert ops.packed_multi_plan([x], [small])["kernel"] == "split-K"
+
+
 def test_refusals(dev):
     import torch
 
