@@ -136,49 +136,64 @@ int launch_wk(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
 }
 
 // One workgroup per CU over all of K (dspark_qmm_cu.h): packed weights, K = 4096, one x for
-// every problem, and 3..6 tiles per CU filling at least 240 CUs; the slices of the split-K
-// plan (8 or 16 groups) fix the association, so the bits are that plan's. Returns the tiles
-// per workgroup, or 0 when the launch takes the split-K kernel.
-int cu_tpw(const dspark_qmm_problem* problems, int count, const long* Ns, long K, const Plan& p) {
-  if (K != kCuK || p.wholek || p.S < 2 || (K / 64) % p.S || ((K / 64) / p.S != 8 && (K / 64) / p.S != 16)) return 0;
+// every problem, TPW = ceil(tiles / 256) row tiles per workgroup split over KH K parts (2 tiles
+// x 4 parts, or 3..6 tiles x 2 parts: 8 or 12 waves), on at least 180 CUs; the slices of the
+// split-K plan fix the association, so the bits are that plan's. Where measured faster than
+// the other kernels: 3..6 tiles (C2 gate+up 25.5 -> 21.3 us, 4-bit 17.9 -> 16.3), and 2 tiles
+// at 8 bits (C2 q+k+v 9.7 -> 9.2 us; at 4 bits 8.3 -> 8.7, not taken). One tile per CU (x 8
+// K parts) measured slower than the whole-K tile kernel (7.9 -> 8.2 us) and is not taken.
+// Returns {TPW, KH}, or {0, 0} when the launch keeps the split-K or whole-K tile kernel.
+struct CuShape {
+  int tpw, kh;
+};
+CuShape cu_shape(const dspark_qmm_problem* problems, int count, const long* Ns, long K, int bits, const Plan& p) {
+  if (K != kCuK || p.wholek) return {0, 0};
+  const long G = K / 64;
+  const long gsl = p.S >= 2 && G % p.S == 0 ? G / p.S : 0;
+  if (gsl != 8 && gsl != 16) return {0, 0};
   long tiles = 0;
   for (int i = 0; i < count; ++i) {
-    if (problems[i].x != problems[0].x || problems[i].ldx != problems[0].ldx) return 0;
+    if (problems[i].x != problems[0].x || problems[i].ldx != problems[0].ldx) return {0, 0};
     tiles += (Ns[i] + 15) / 16;
   }
   const long tpw = (tiles + kCUs - 1) / kCUs;
-  if (tpw < 3 || tpw > 6 || (tiles + tpw - 1) / tpw < 240) return 0;
-  return (int)tpw;
+  if (tpw < 2 || tpw > 6 || (tpw == 2 && bits != 8) || (tiles + tpw - 1) / tpw < 180) return {0, 0};
+  const int kh = tpw == 2 ? 4 : 2;
+  if ((G / kh) % gsl) return {0, 0};
+  return {(int)tpw, kh};
 }
 
-template <int BITS, int TPW, int GSL>
+template <int BITS, int TPW, int KH, int GSL>
 int launch_cu_t(const QmmSkArgs& a, const Plan& p, int tiles, hipStream_t st) {
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_cu_kernel<BITS, TPW, GSL>),
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_cu_kernel<BITS, TPW, KH, GSL>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)cu_lds_bytes(TPW));
   });
   if (attr != hipSuccess) return fail(DSPARK_ERR_LAUNCH, "dspark_qmm_packed: LDS attribute: %s", hipGetErrorString(attr));
-  hipLaunchKernelGGL((qmm_cu_kernel<BITS, TPW, GSL>), dim3((unsigned)((tiles + TPW - 1) / TPW), p.mtiles),
-                     dim3(128 * TPW), cu_lds_bytes(TPW), st, a, tiles);
+  hipLaunchKernelGGL((qmm_cu_kernel<BITS, TPW, KH, GSL>), dim3((unsigned)((tiles + TPW - 1) / TPW), p.mtiles),
+                     dim3(64 * TPW * KH), cu_lds_bytes(TPW), st, a, tiles);
   return check_launch("dspark_qmm_packed");
 }
 
 template <int BITS, int GSL>
-int launch_cu_g(const QmmSkArgs& a, const Plan& p, int tpw, int tiles, hipStream_t st) {
-  switch (tpw) {
-    case 3: return launch_cu_t<BITS, 3, GSL>(a, p, tiles, st);
-    case 4: return launch_cu_t<BITS, 4, GSL>(a, p, tiles, st);
-    case 5: return launch_cu_t<BITS, 5, GSL>(a, p, tiles, st);
-    default: return launch_cu_t<BITS, 6, GSL>(a, p, tiles, st);
+int launch_cu_g(const QmmSkArgs& a, const Plan& p, CuShape c, int tiles, hipStream_t st) {
+  switch (c.tpw) {
+    case 2: return launch_cu_t<BITS, 2, 4, GSL>(a, p, tiles, st);
+    case 3: return launch_cu_t<BITS, 3, 2, GSL>(a, p, tiles, st);
+    case 4: return launch_cu_t<BITS, 4, 2, GSL>(a, p, tiles, st);
+    case 5: return launch_cu_t<BITS, 5, 2, GSL>(a, p, tiles, st);
+    case 6: return launch_cu_t<BITS, 6, 2, GSL>(a, p, tiles, st);
+    default: break;
   }
+  return fail(DSPARK_ERR_SHAPE, "dspark_qmm_packed: no per-CU instance for %d tiles per workgroup", c.tpw);
 }
 
-int launch_cu(const QmmSkArgs& a, const Plan& p, int bits, long G, int tpw, int tiles, hipStream_t st) {
-  const bool g16 = G / p.S == 16;
-  if (bits == 8) return g16 ? launch_cu_g<8, 16>(a, p, tpw, tiles, st) : launch_cu_g<8, 8>(a, p, tpw, tiles, st);
-  return g16 ? launch_cu_g<4, 16>(a, p, tpw, tiles, st) : launch_cu_g<4, 8>(a, p, tpw, tiles, st);
+int launch_cu(const QmmSkArgs& a, const Plan& p, int bits, CuShape c, int tiles, hipStream_t st) {
+  const bool g16 = (kCuK / 64) / p.S == 16;
+  if (bits == 8) return g16 ? launch_cu_g<8, 16>(a, p, c, tiles, st) : launch_cu_g<8, 8>(a, p, c, tiles, st);
+  return g16 ? launch_cu_g<4, 16>(a, p, c, tiles, st) : launch_cu_g<4, 8>(a, p, c, tiles, st);
 }
 
 template <int BITS, bool SWIGLU = false>
@@ -391,6 +406,16 @@ int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bit
     a.p[i] = a.p[0];
     a.p[i].strip0 = 1 << 30;
   }
+  if (packed) {
+    if (const CuShape c = cu_shape(problems, count, Ns, K, bits, p); c.tpw) {  // blockIdx.x counts TPW-tile groups
+      int t0 = 0;
+      for (int i = 0; i < count; ++i) {
+        a.p[i].strip0 = t0;
+        t0 += (int)((problems[i].N + 15) / 16);
+      }
+      return launch_cu(a, p, bits, c, t0, s);
+    }
+  }
   if (p.wholek) {  // blockIdx.x counts 16-row tiles
     int t0 = 0;
     for (int i = 0; i < count; ++i) {
@@ -400,17 +425,7 @@ int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bit
     if (packed) return launch_wk<true, true>(a, p, s);
     return sbvec ? launch_wk<false, true>(a, p, s) : launch_wk<false, false>(a, p, s);
   }
-  if (packed) {
-    if (const int tpw = cu_tpw(problems, count, Ns, K, p)) {  // blockIdx.x counts TPW-tile groups
-      int t0 = 0;
-      for (int i = 0; i < count; ++i) {
-        a.p[i].strip0 = t0;
-        t0 += (int)((problems[i].N + 15) / 16);
-      }
-      return launch_cu(a, p, bits, G, tpw, t0, s);
-    }
-    return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
-  }
+  if (packed) return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
   return bits == 4 ? launch_bits<4>(a, p, sbvec, s) : launch_bits<8>(a, p, sbvec, s);
 }
 
@@ -613,13 +628,13 @@ extern "C" int dspark_qmm_packed_multi_plan(const dspark_qmm_packed_problem* pro
   if (st || (st = validate(views, count, M, bits, group_size, Ns, true))) return st;
   const Plan p = make_plan(Ns, count, views[0].K, M, bits, true);
   if (p.S == 0) return fail(DSPARK_ERR_SHAPE, "qmm_plan: shape refused");
-  const int tpw = cu_tpw(views, count, Ns, views[0].K, p);
+  const CuShape c = cu_shape(views, count, Ns, views[0].K, bits, p);
   long tiles = 0;
   for (int i = 0; i < count; ++i) tiles += (Ns[i] + 15) / 16;
-  out[0] = p.wholek ? 1 : tpw ? 2 : 0;
+  out[0] = p.wholek ? 1 : c.tpw ? 2 : 0;
   out[1] = p.S;
-  out[2] = tpw;
-  out[3] = p.wholek ? p.tiles * p.mtiles : tpw ? (int)((tiles + tpw - 1) / tpw) * p.mtiles : p.S * p.strips * p.mtiles;
+  out[2] = c.tpw;
+  out[3] = c.tpw ? (int)((tiles + c.tpw - 1) / c.tpw) * p.mtiles : p.wholek ? p.tiles * p.mtiles : p.S * p.strips * p.mtiles;
   return DSPARK_OK;
 }
 

@@ -1,20 +1,20 @@
 // Dense small-M affine qmm, one workgroup per CU over all of K (gfx950), for packed weights
-// with K = 4096 and three to six 16-row tiles per CU (the 8B-class MLP's gate+up pair: 1536
-// tiles, six per CU).
+// with K = 4096 and one to six 16-row tiles per CU (the 8B-class MLP's gate+up pair: 1536
+// tiles, six per CU; a [4096, 4096] matrix: one per CU).
 //
-// A workgroup of TPW * 2 waves owns TPW consecutive 16-row tiles; wave w works tile w % TPW
-// over K half w / TPW (32 groups). The 16 rows of x (128 KB) and the tiles' scale/bias blocks go
-// straight into LDS (global_load_lds_dwordx4, no registers) first, so the CU's in-order request
-// stream carries x once, ahead of the weights. Each wave then keeps 8 groups of weights in
-// flight: it requests its first 8 groups, and one more group each time it multiplies one, so
-// no wave stalls issuing far ahead of its work, the three waves of a SIMD multiply side by side
-// as their groups land, and there is no split-K exchange at all. (Requesting a wave's whole
-// half tile at once stalled the issue behind the CU's full request queue and left each SIMD
-// multiplying one wave after another: slower than split-K.)
+// A workgroup of TPW * KH waves owns TPW consecutive 16-row tiles; wave w works tile w % TPW
+// over K part w / TPW (64 / KH groups). The 16 rows of x (128 KB) and the tiles' scale/bias
+// blocks go straight into LDS (global_load_lds_dwordx4, no registers) first, so the CU's
+// in-order request stream carries x once, ahead of the weights. Each wave then keeps 8 groups
+// of weights in flight: it requests its first 8 groups, and one more group each time it
+// multiplies one, so no wave stalls issuing far ahead of its work, the waves of a SIMD multiply
+// side by side as their groups land, and there is no split-K exchange at all. (Requesting a
+// wave's whole part at once stalled the issue behind the CU's full request queue and left each
+// SIMD multiplying one wave after another: slower than split-K.)
 //
 // Bitwise the split-K kernel's results (dspark_qmm_splitk.h) for the same slice count S: the
 // per-group arithmetic is the same (acc = fma(b, sum x, fma(s, P, acc)), P from the same two
-// MFMAs), each wave keeps one accumulator per split-K slice of its half (acc from zero at the
+// MFMAs), each wave keeps one accumulator per split-K slice of its part (acc from zero at the
 // slice's first group), the group sums of x are formed in the staging kernel's order (8-value
 // chunk sums, then the 8 chunks pairwise), and the slice accumulators are summed in slice order
 // from zero before the bf16 rounding, as the split-K last arriver does.
@@ -33,16 +33,16 @@ constexpr size_t cu_lds_bytes(int tpw) {
 
 // GSL: groups per split-K slice (8, 16 or 32). Tiles are numbered across the problems
 // (args.p[i].strip0 = first tile of problem i); every problem reads the same x.
-template <int BITS, int TPW, int GSL>
-__global__ __launch_bounds__(128 * TPW) void qmm_cu_kernel(const QmmSkArgs args, int tiles) {
-  constexpr int NW = 2 * TPW;
+template <int BITS, int TPW, int KH, int GSL>
+__global__ __launch_bounds__(64 * TPW * KH) void qmm_cu_kernel(const QmmSkArgs args, int tiles) {
+  constexpr int NW = KH * TPW;
   constexpr int G = kCuK / 64;           // 64 groups
-  constexpr int GPW = G / 2;             // groups per wave (its half of K)
+  constexpr int GPW = G / KH;            // groups per wave (its part of K)
   constexpr int SPW = GPW / GSL;         // split-K slices per wave
   constexpr int S = G / GSL;
   constexpr int XP = kCuXPitch;
   constexpr int OCT = G / 8;             // scale/bias octets per tile
-  static_assert(GPW % GSL == 0 && GSL % 2 == 0, "slices within a half");
+  static_assert(GPW % GSL == 0 && GSL % 2 == 0, "slices within a K part");
   extern __shared__ __attribute__((aligned(16))) char lds[];
   u16* const xs = reinterpret_cast<u16*>(lds);                          // [16][XP]
   char* const sbl = lds + 16 * XP * 2;                                  // [TPW][OCT][512 B]
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(128 * TPW) void qmm_cu_kernel(const QmmSkArgs args,
                                        0);
     }
   }
-  // ---- 2. the first PF weight fragments of this wave's half tile; the rest are requested one
+  // ---- 2. the first PF weight fragments of this wave's part of its tile; the rest are requested one
   // per group as the multiply consumes them, so a wave never stalls issuing far ahead of its
   // work and the copies into LDS land before most weight requests are queued
   __builtin_amdgcn_sched_barrier(0);
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(128 * TPW) void qmm_cu_kernel(const QmmSkArgs args,
     constexpr int GPL = BITS == 4 ? 2 : 1;  // groups per load
 #pragma unroll
     for (int h = 0; h < GPL; ++h) {
-      const int gw = GPL * j + h;  // group within the wave's half
+      const int gw = GPL * j + h;  // group within the wave's K part
       const int g = kp * GPW + gw;
       if (gw % GSL == 0) acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
       const char* sbo = sb_t + (g >> 3) * 512 + 2 * (g & 7);
@@ -166,8 +166,8 @@ __global__ __launch_bounds__(128 * TPW) void qmm_cu_kernel(const QmmSkArgs args,
     }
   }
 
-  // ---- 5. the slice accumulators of the tile's two halves meet in LDS (x's area, free once
-  // every wave is done multiplying); the wave of the first half sums them in slice order
+  // ---- 5. the slice accumulators of the tile's K parts meet in LDS (x's area, free once
+  // every wave is done multiplying); the wave of the first part sums them in slice order
   __syncthreads();
   f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);  // [TPW][S][64 lanes]
 #pragma unroll

@@ -149,6 +149,28 @@ def test_per_cu_kernel_bit_identical_to_split_k(dev, bits, ns):
                     assert_rms_close(yh[:, sl], want, 2e-2, f"per-CU {bits}-bit {ns} rows {sl}")
 
 
+@pytest.mark.parametrize("m", [1, 16, 33])
+def test_per_cu_kernel_two_tiles_8bit(dev, m):
+    """The q/k/v launch of an 8B-shaped layer (384 tiles: two per workgroup, K in four parts)
+    takes the per-CU kernel at 8 bits only; its bits are the split-K launch's."""
+    import torch
+
+    from dspark_rocm import ops
+
+    k, ns = 4096, (4096, 1024, 1024)
+    x = to_dev_bf16(randn_bf16(rng(m + 77), m, k), dev)
+    for bits, kernel in ((8, "whole-K per CU"), (4, "split-K")):
+        devs = [_dev(*_quantized(60 + i + bits, n, k, bits), dev) for i, n in enumerate(ns)]
+        packs = [ops.qmm_pack(*d, bits=bits) for d in devs]
+        plan = ops.packed_multi_plan([x], packs)
+        assert plan["kernel"] == kernel, plan
+        got = ops.quantized_matmul_packed_multi([x], packs)
+        want = ops.quantized_matmul_multi([x], [d[0] for d in devs], [d[1] for d in devs], [d[2] for d in devs],
+                                          bits=bits)
+        for y, w in zip(got, want):
+            assert torch.equal(y, w), (bits, m)
+
+
 def test_per_cu_kernel_needs_one_x(dev):
     """Problems reading different x tensors, or a launch of too few tiles, keep the split-K
     kernel."""
