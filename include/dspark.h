@@ -431,6 +431,13 @@ int dspark_moe_switch_glu_packed(const void* x, const void* logits, int64_t M, i
                                  int32_t* inds, void* scores, void* workspace, size_t workspace_bytes,
                                  dspark_stream stream);
 
+/* Which expert kernel dspark_moe_switch_glu_packed launches for a shape (no counterpart in the
+ * reference; for tests and profiles): out[0] for gate/up, out[1] for down, 1 = one workgroup per
+ * CU over a contiguous range of (live expert, 16-column strip) units (M <= 16 tokens, E <= 256,
+ * M * k <= 512, gate/up K = H in {512, 2048}, down K = I in {256, 768}), 0 = one workgroup per
+ * (expert, strip). */
+int dspark_moe_packed_plan(int64_t M, int64_t H, int64_t I, int64_t E, int64_t k, int bits, int32_t* out);
+
 /* ------------------------------------------------------------------ verify-forward layer kernels */
 
 /*

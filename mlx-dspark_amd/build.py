@@ -41,6 +41,14 @@ HIPCC_FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
+# Extra flags of single translation units
+FILE_FLAGS = {
+    # the per-CU MoE expert kernel unrolls its unit loops in full (up to 68 steps of one 1 KB
+    # load each), past LLVM's default full-unroll threshold; a loop left partly rolled would
+    # index the kernel's load window at run time and keep it in scratch memory
+    "dspark_moe_cu.hip": ["-mllvm", "-pragma-unroll-threshold=200000"],
+}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -54,7 +62,7 @@ def sources() -> list[str]:
 
 
 def _compile(src: str, obj: str, verbose: bool) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -18,6 +18,7 @@
 // expert's weight tile is streamed once for all of its tokens (<= 16 at verify widths).
 #include <initializer_list>
 
+#include "dspark_moe_cu.h"
 #include "dspark_moe_rc.h"
 #include "dspark_moe_sk.h"
 
@@ -538,6 +539,31 @@ int launch_moe_sk(const MoeSkArgs& a, const MoePlan& p, int E, int bits, hipStre
   return check_launch(SWIGLU ? "moe gate/up" : "moe down");
 }
 
+// The per-CU gate/up kernel's arguments (the small-bucket kernel's, plus the routing's pair order
+// and the expert stride of the packed weights)
+MoeCuArgs cu_args(const MoeSkArgs& g, const int* sorted, long M, long E, long k, int bits) {
+  MoeCuArgs a{};
+  a.x = g.x;
+  a.sorted = sorted;
+  a.offsets = g.offsets;
+  a.wg = reinterpret_cast<const char*>(g.w0);
+  a.sg = g.s0;
+  a.bg = g.b0;
+  a.wu = reinterpret_cast<const char*>(g.w1);
+  a.su = g.s1;
+  a.bu = g.b1;
+  a.h = g.y;
+  a.ldx = g.ldx;
+  a.ldh = g.ldy;
+  a.wstride = (long)g.N * g.K * bits / 8;
+  a.M = (int)M;
+  a.E = (int)E;
+  a.N = g.N;
+  a.k = (int)k;
+  a.strips = g.N / 16;
+  return a;
+}
+
 }  // namespace
 }  // namespace dspark
 
@@ -677,7 +703,9 @@ int switch_glu_impl(const void* x, const void* logits, int64_t M, int64_t H, int
     return fail(DSPARK_ERR_UNSUPPORTED,
                 "moe_switch_glu_packed: H=%lld I=%lld need K %% 128 == 0 and 16-byte aligned scales and biases",
                 (long long)H, (long long)I);
-  if (packed) {
+  if (packed && moe_cu_gate_up(M, H, I, E, k, bits)) {
+    if ((st = launch_moe_cu(cu_args(g, sorted, M, E, k, bits), H, bits, s))) return st;
+  } else if (packed) {
     if ((st = launch_moe_rc<true, true>(rc_args(g), rgu, (int)E, bits, s))) return st;
   } else if (rgu.kw && rgu2.kw) {
     if ((st = launch_moe_rc<true>(rc_args(g), rgu, (int)E, bits, s))) return st;

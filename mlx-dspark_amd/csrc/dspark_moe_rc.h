@@ -8,9 +8,9 @@
 // even tiles read gate rows, odd tiles the up rows of the same 16 columns, and the strip's
 // reduced tiles become h = swiglu(gate, up).
 // The bucket's rows go through the MFMA in passes of RC = 4: x rows are gathered into LDS
-// (4 rows x K, with their per-group sums) and MFMA A rows 4..15 repeat row 3; their outputs
-// are dropped. One pass covers buckets of up to 4 rows; larger tiles loop, reusing the
-// weights held in registers.
+// (4 rows x K, with their per-group sums; rows past the bucket are not read and staged as
+// zeros) and MFMA A rows 4..15 repeat row 3; their outputs are dropped. One pass covers buckets
+// of up to 4 rows; larger tiles loop, reusing the weights held in registers.
 // Issue order of a workgroup: bucket bounds -> x row indices (pass 0) -> every weight load
 // -> the tiles' scale and bias rows (contiguous 16-byte chunks, one or two per thread, kept in
 // LDS) -> x loads (waiting only for the row indices, which were issued first)
@@ -126,10 +126,14 @@ __global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_r
     const long off = min((long)n0 * G + 8 * cc, (long)N * G - 8);  // in bounds of expert e's block
     sbv[j] = ldg128(base + e * sstride + off);
   }
-  // ---- 4. x rows of pass 0 (waits only for the row indices, issued first)
+  // ---- 4. x rows of pass 0 (waits only for the row indices, issued first). Only the bucket's
+  // rows are read: rows past it are staged as zeros (their MFMA rows are dropped)
   u32x4_t xv[XCH];
 #pragma unroll
-  for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
+  for (int i = 0; i < XCH; ++i) {
+    xv[i] = u32x4_t{0u, 0u, 0u, 0u};
+    if (xrow[i] < m_rows) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
+  }
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (BITS == 4 && !PW) swap_pairs(wsl);  // the packed form is stored swapped
 
@@ -143,7 +147,10 @@ __global__ __launch_bounds__(256, (KSMAX >= 24 || BITS == 8) ? 2 : 3) void moe_r
 #pragma unroll
       for (int i = 0; i < XCH; ++i) src[i] = src_row(r0, xrow[i]);
 #pragma unroll
-      for (int i = 0; i < XCH; ++i) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
+      for (int i = 0; i < XCH; ++i) {
+        xv[i] = u32x4_t{0u, 0u, 0u, 0u};
+        if (r0 + xrow[i] < m_rows) xv[i] = ldg128(a.x + (long)src[i] * a.ldx + 8 * xcol[i]);
+      }
       __syncthreads();  // the previous pass has finished with xs, xsum and red
     }
     // ---- 5. x rows -> LDS with their per-group sums (8 lanes per (row, group))

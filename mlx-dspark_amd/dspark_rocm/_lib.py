@@ -146,6 +146,7 @@ SIGNATURES: dict[str, tuple] = {
                                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                              c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                                              c_void_p, c_void_p, c_size_t, c_void_p]),
+    "dspark_moe_packed_plan": (c_int, [c_i64, c_i64, c_i64, c_i64, c_i64, c_int, ctypes.POINTER(ctypes.c_int32)]),
     "dspark_rmsnorm": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_float, c_void_p, c_i64,
                                c_void_p, c_i64, c_void_p]),
     "dspark_qk_norm_rope_kv": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64,

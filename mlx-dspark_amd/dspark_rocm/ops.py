@@ -599,6 +599,17 @@ def moe_packable(experts: int, n: int, k: int, bits: int, group_size: int = GROU
     return int(_lib.load().dspark_moe_packed_bytes(experts, n, k, bits, group_size)) > 0
 
 
+MOE_KERNELS = ("expert x strip", "per CU")
+
+
+def moe_packed_plan(M: int, H: int, I: int, E: int, k: int, bits: int) -> dict:
+    """The expert kernels ``moe_switch_glu`` runs over packed experts for this shape (host-only
+    query): ``gate_up`` and ``down``, each one of ``MOE_KERNELS``."""
+    out = (ctypes.c_int32 * 2)()
+    _lib.call("dspark_moe_packed_plan", M, H, I, E, k, bits, out)
+    return {"gate_up": MOE_KERNELS[out[0]], "down": MOE_KERNELS[out[1]]}
+
+
 def moe_pack(w: torch.Tensor, *, bits: int, group_size: int = GROUP) -> PackedExperts:
     """Pack stacked expert weights (int32 [E, N, K*bits/32]) once (N % 16 == 0, K % 128 == 0)."""
     _require_cuda(w)

@@ -50,6 +50,25 @@ def test_shape_queries_without_gpu():
     assert lib.dspark_last_error() is not None
 
 
+def test_moe_packed_plan_picks_the_per_cu_kernel_for_verify_widths():
+    """The packed MoE block runs its gate/up projection one workgroup per CU for M <= 16 tokens,
+    E <= 256, M * k <= 512 and the instantiated widths (K = H in {512, 2048}); every other shape,
+    and the down projection always, keeps one workgroup per (expert, strip)."""
+    from dspark_rocm import ops
+
+    cu, rc = ops.MOE_KERNELS[1], ops.MOE_KERNELS[0]
+    for bits in (4, 8):
+        assert ops.moe_packed_plan(16, 2048, 768, 128, 8, bits) == {"gate_up": cu, "down": rc}
+        assert ops.moe_packed_plan(1, 2048, 768, 256, 8, bits) == {"gate_up": cu, "down": rc}
+        assert ops.moe_packed_plan(16, 512, 256, 2, 2, bits) == {"gate_up": cu, "down": rc}
+        assert ops.moe_packed_plan(16, 2048, 1536, 128, 8, bits) == {"gate_up": cu, "down": rc}
+        assert ops.moe_packed_plan(17, 2048, 768, 128, 8, bits)["gate_up"] == rc   # M > 16
+        assert ops.moe_packed_plan(16, 2048, 768, 257, 8, bits)["gate_up"] == rc   # E > 256
+        assert ops.moe_packed_plan(16, 2048, 768, 128, 33, bits)["gate_up"] == rc  # M * k > 512
+        assert ops.moe_packed_plan(16, 256, 128, 8, 2, bits)["gate_up"] == rc
+        assert ops.moe_packed_plan(16, 4096, 768, 128, 8, bits)["gate_up"] == rc
+
+
 def test_plan_blocks_scale_with_length():
     from dspark_rocm import _lib
 

@@ -111,15 +111,26 @@ def test_switch_glu(dev, M, E, k, H, I, bits):
 
 @pytest.mark.parametrize("M,E,k,H,I,bits", [(16, 8, 2, 256, 128, 4), (16, 128, 8, 2048, 768, 4),
                                              (16, 128, 8, 2048, 768, 8), (16, 2, 2, 512, 256, 4),
+                                             (16, 2, 2, 512, 256, 8),
+                                             (1, 128, 8, 2048, 768, 4),     # 8 one-row buckets
+                                             (5, 128, 8, 2048, 768, 8),
+                                             (16, 256, 8, 2048, 768, 4),    # E = 256: four ballots
+                                             (7, 64, 6, 512, 256, 4),
                                              (33, 4, 2, 256, 4096, 8)])
 def test_switch_glu_packed_experts_bitwise(dev, M, E, k, H, I, bits):
     """The packed expert form (dspark_moe_pack) gives the row-major block's output bit for bit
     (same K parts, same per-group arithmetic and order), and its bytes are the weight part of the
-    dense packed layout of each expert's matrix."""
+    dense packed layout of each expert's matrix. For M <= 16 and H in {512, 2048} the packed
+    block's gate/up runs one workgroup per CU (ops.moe_packed_plan) and the row-major block's one
+    workgroup per (expert, strip): the two kernels agree bit for bit, 16-row buckets (E = 2) and
+    one-row buckets (M = 1) included."""
     import torch
 
     from dspark_rocm import ops
     from test_gpu_qmm_packed import _pack_np
+
+    plan = ops.moe_packed_plan(M, H, I, E, k, bits)
+    assert plan["gate_up"] == ("per CU" if M <= 16 and H in (512, 2048) else "expert x strip")
 
     r = rng(M + E + H + 1)
     x = to_dev_bf16(randn_bf16(r, M, H), dev)
