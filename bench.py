@@ -106,7 +106,7 @@ def gate_up_kernel_name(ls) -> str:
     P = ls.packs[0]
     p = ops.packed_multi_plan([ls.x["gu"]], [P["gate"], P["up"]])
     k = P["gate"].k
-    if p["kernel"] == "whole-K per CU":
+    if p["kernel"] == "per CU":
         name = f"qmm_cu_kernel<{ls.bits},{p['tiles_per_workgroup']},{k // 64 // p['slices']}>"
     elif p["kernel"] == "whole-K tile":
         name = f"qmm_wk_kernel<{ls.bits},8,true,true>"

@@ -223,12 +223,13 @@ size_t dspark_qmm_packed_multi_workspace(const dspark_qmm_packed_problem* proble
 
 /* Which kernel dspark_qmm_packed_multi runs for these problems (host-only query, no GPU work):
  * out[0] 0 = split-K, 1 = one 16-row tile per workgroup over all of K, 2 = one workgroup per
- * CU over all of K (K = 4096, one x for every problem, 3..6 row tiles per CU, or 2 at 8 bits);
- * out[1] the K
- * slices S whose association the result follows (every kernel gives the split-K plan's bits for
- * the same S, the second one where the group sums of x are exact in fp32); out[2] row tiles per
- * workgroup (kind 2, else 0); out[3] workgroups. Mirrors skinny_qmm.plan (skinny_qmm.py:190-237)
- * for the packed form. Returns a dspark_status. */
+ * CU (one x for every problem; K = 4096 with 3..6 row tiles per CU, or 2 at 8 bits, over all of
+ * K; K = 12288 with 4 row tiles per CU over a quarter of K each); out[1] the K slices S whose
+ * association the result follows (every kernel gives the split-K plan's bits for the same S,
+ * the second one where the group sums of x are exact in fp32); out[2] row tiles per workgroup
+ * (kind 2, else 0); out[3] workgroups; out[4] workgroups per row tile along K (kind 2, else 0).
+ * Mirrors skinny_qmm.plan (skinny_qmm.py:190-237) for the packed form. Returns a
+ * dspark_status. */
 int dspark_qmm_packed_multi_plan(const dspark_qmm_packed_problem* problems, int count, int64_t M, int bits,
                                  int group_size, int32_t out[4]);
 

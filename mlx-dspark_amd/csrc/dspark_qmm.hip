@@ -135,50 +135,62 @@ int launch_wk(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
   return check_launch(PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
 }
 
-// One workgroup per CU over all of K (dspark_qmm_cu.h): packed weights, K = 4096, one x for
-// every problem, TPW = ceil(tiles / 256) row tiles per workgroup split over KH K parts (2 tiles
-// x 4 parts, or 3..6 tiles x 2 parts: 8 or 12 waves), on at least 180 CUs; the slices of the
-// split-K plan fix the association, so the bits are that plan's. Where measured faster than
-// the other kernels: 3..6 tiles (C2 gate+up 25.5 -> 21.3 us, 4-bit 17.9 -> 16.3), and 2 tiles
-// at 8 bits (C2 q+k+v 9.7 -> 9.2 us; at 4 bits 8.3 -> 8.7, not taken). One tile per CU (x 8
-// K parts) measured slower than the whole-K tile kernel (7.9 -> 8.2 us) and is not taken.
-// Returns {TPW, KH}, or {0, 0} when the launch keeps the split-K or whole-K tile kernel.
+// One workgroup per CU (dspark_qmm_cu.h): packed weights, one x for every problem, TPW row
+// tiles per workgroup split over KH K parts, on at least 180 CUs; the slices of the split-K plan
+// fix the association, so the bits are that plan's.
+//   K = 4096: TPW = ceil(tiles / 256) (2 tiles x 4 parts, or 3..6 tiles x 2 parts: 8 or 12
+//   waves) over all of K. Where measured faster than the other kernels: 3..6 tiles (C2 gate+up
+//   25.5 -> 21.3 us, 4-bit 17.9 -> 16.3), and 2 tiles at 8 bits (C2 q+k+v 9.7 -> 9.2 us; at 4
+//   bits 8.3 -> 8.7, not taken). One tile per CU (x 8 K parts) measured slower than the whole-K
+//   tile kernel (7.9 -> 8.2 us) and is not taken.
+//   K = 12288 with 16-group slices, up to 256 tiles (C2 down): four workgroups per tile group,
+//   each over 3072 columns of K (three slices), 4 tiles x 3 waves, their partials summed by the
+//   last to arrive. (Three parts of 4096 at 3 tiles per workgroup would need 258 workgroups.)
+// Returns the shape, or tpw = 0 when the launch keeps the split-K or whole-K tile kernel.
 struct CuShape {
-  int tpw, kh;
+  int tpw, kh, kparts, kc;
 };
 CuShape cu_shape(const dspark_qmm_problem* problems, int count, const long* Ns, long K, int bits, const Plan& p) {
-  if (K != kCuK || p.wholek) return {0, 0};
+  if (p.wholek) return {0, 0, 0, 0};
   const long G = K / 64;
   const long gsl = p.S >= 2 && G % p.S == 0 ? G / p.S : 0;
-  if (gsl != 8 && gsl != 16) return {0, 0};
+  if (gsl != 8 && gsl != 16) return {0, 0, 0, 0};
   long tiles = 0;
   for (int i = 0; i < count; ++i) {
-    if (problems[i].x != problems[0].x || problems[i].ldx != problems[0].ldx) return {0, 0};
+    if (problems[i].x != problems[0].x || problems[i].ldx != problems[0].ldx) return {0, 0, 0, 0};
     tiles += (Ns[i] + 15) / 16;
   }
+  if (K == 12288 && gsl == 16 && tiles <= kCUs && (tiles + 3) / 4 * 4 >= 180) return {4, 3, 4, 3072};
+  if (K != kCuK) return {0, 0, 0, 0};
   const long tpw = (tiles + kCUs - 1) / kCUs;
-  if (tpw < 2 || tpw > 6 || (tpw == 2 && bits != 8) || (tiles + tpw - 1) / tpw < 180) return {0, 0};
+  if (tpw < 2 || tpw > 6 || (tpw == 2 && bits != 8) || (tiles + tpw - 1) / tpw < 180) return {0, 0, 0, 0};
   const int kh = tpw == 2 ? 4 : 2;
-  if ((G / kh) % gsl) return {0, 0};
-  return {(int)tpw, kh};
+  if ((G / kh) % gsl) return {0, 0, 0, 0};
+  return {(int)tpw, kh, 1, (int)kCuK};
 }
 
-template <int BITS, int TPW, int KH, int GSL>
+template <int BITS, int TPW, int KH, int GSL, int KC = kCuK, int KP = 1>
 int launch_cu_t(const QmmSkArgs& a, const Plan& p, int tiles, hipStream_t st) {
+  constexpr size_t lds = cu_lds_bytes(TPW, KC);
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_cu_kernel<BITS, TPW, KH, GSL>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)cu_lds_bytes(TPW));
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_cu_kernel<BITS, TPW, KH, GSL, KC, KP>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   });
   if (attr != hipSuccess) return fail(DSPARK_ERR_LAUNCH, "dspark_qmm_packed: LDS attribute: %s", hipGetErrorString(attr));
-  hipLaunchKernelGGL((qmm_cu_kernel<BITS, TPW, KH, GSL>), dim3((unsigned)((tiles + TPW - 1) / TPW), p.mtiles),
-                     dim3(64 * TPW * KH), cu_lds_bytes(TPW), st, a, tiles);
+  hipLaunchKernelGGL((qmm_cu_kernel<BITS, TPW, KH, GSL, KC, KP>),
+                     dim3((unsigned)((tiles + TPW - 1) / TPW), p.mtiles, (unsigned)KP), dim3(64 * TPW * KH), lds, st, a,
+                     tiles);
   return check_launch("dspark_qmm_packed");
 }
 
 template <int BITS, int GSL>
 int launch_cu_g(const QmmSkArgs& a, const Plan& p, CuShape c, int tiles, hipStream_t st) {
+  if (c.kc == 3072) {
+    if constexpr (GSL == 16) return launch_cu_t<BITS, 4, 3, 16, 3072, 4>(a, p, tiles, st);
+    return fail(DSPARK_ERR_SHAPE, "dspark_qmm_packed: no per-CU instance for 3072-column parts of %d groups", GSL);
+  }
   switch (c.tpw) {
     case 2: return launch_cu_t<BITS, 2, 4, GSL>(a, p, tiles, st);
     case 3: return launch_cu_t<BITS, 3, 2, GSL>(a, p, tiles, st);
@@ -191,7 +203,7 @@ int launch_cu_g(const QmmSkArgs& a, const Plan& p, CuShape c, int tiles, hipStre
 }
 
 int launch_cu(const QmmSkArgs& a, const Plan& p, int bits, CuShape c, int tiles, hipStream_t st) {
-  const bool g16 = (kCuK / 64) / p.S == 16;
+  const bool g16 = (a.p[0].K / 64) / p.S == 16;
   if (bits == 8) return g16 ? launch_cu_g<8, 16>(a, p, c, tiles, st) : launch_cu_g<8, 8>(a, p, c, tiles, st);
   return g16 ? launch_cu_g<4, 16>(a, p, c, tiles, st) : launch_cu_g<4, 8>(a, p, c, tiles, st);
 }
@@ -634,7 +646,9 @@ extern "C" int dspark_qmm_packed_multi_plan(const dspark_qmm_packed_problem* pro
   out[0] = p.wholek ? 1 : c.tpw ? 2 : 0;
   out[1] = p.S;
   out[2] = c.tpw;
-  out[3] = c.tpw ? (int)((tiles + c.tpw - 1) / c.tpw) * p.mtiles : p.wholek ? p.tiles * p.mtiles : p.S * p.strips * p.mtiles;
+  out[3] = c.tpw ? (int)((tiles + c.tpw - 1) / c.tpw) * p.mtiles * c.kparts
+                 : p.wholek ? p.tiles * p.mtiles : p.S * p.strips * p.mtiles;
+  out[4] = c.tpw ? c.kparts : 0;
   return DSPARK_OK;
 }
 

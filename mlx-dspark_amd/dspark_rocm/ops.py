@@ -206,18 +206,19 @@ def _packed_problems(x_list, packed_list, outs):
     return probs, cnt, m, bits, results, keep
 
 
-PACKED_KERNELS = ("split-K", "whole-K tile", "whole-K per CU")
+PACKED_KERNELS = ("split-K", "whole-K tile", "per CU")
 
 
 def packed_multi_plan(x_list, packed_list, *, group_size: int = GROUP) -> dict:
     """The kernel ``quantized_matmul_packed_multi`` runs for these operands (host-only query):
     ``kernel`` (one of ``PACKED_KERNELS``), ``slices`` (the split-K association the bits
-    follow), ``tiles_per_workgroup`` (per-CU kernel) and ``workgroups``."""
+    follow), ``tiles_per_workgroup`` and ``k_parts`` (per-CU kernel: workgroups per row tile
+    along K) and ``workgroups``."""
     probs, cnt, m, bits, _, keep = _packed_problems(x_list, packed_list, None)
-    out = (ctypes.c_int32 * 4)()
+    out = (ctypes.c_int32 * 5)()
     _lib.call("dspark_qmm_packed_multi_plan", probs, cnt, m, bits, group_size, out)
     return {"kernel": PACKED_KERNELS[out[0]], "slices": out[1], "tiles_per_workgroup": out[2],
-            "workgroups": out[3]}
+            "workgroups": out[3], "k_parts": out[4]}
 
 
 def quantized_matmul_packed_multi(x_list, packed_list, *, group_size: int = GROUP, outs=None,

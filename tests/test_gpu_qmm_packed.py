@@ -134,7 +134,7 @@ def test_per_cu_kernel_bit_identical_to_split_k(dev, bits, ns):
         for xd in (to_dev_bf16(x, dev), wide[:, 32:32 + k]):   # contiguous rows, then ldx = K + 64
             plan = ops.packed_multi_plan([xd], packs)
             tiles = sum((n + 15) // 16 for n in ns)
-            assert plan["kernel"] == "whole-K per CU", plan
+            assert plan["kernel"] == "per CU" and plan["k_parts"] == 1, plan
             assert plan["tiles_per_workgroup"] == -(-tiles // 256)
             got = ops.quantized_matmul_packed_multi([xd], packs)
             want = ops.quantized_matmul_multi([xd], [d[0] for d in devs], [d[1] for d in devs],
@@ -149,6 +149,37 @@ def test_per_cu_kernel_bit_identical_to_split_k(dev, bits, ns):
                     assert_rms_close(yh[:, sl], want, 2e-2, f"per-CU {bits}-bit {ns} rows {sl}")
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_per_cu_kernel_k_parts_bit_identical_to_split_k(dev, bits):
+    """The down launch of an 8B-shaped layer ([4096, 12288]: 256 row tiles, 12 slices of 16
+    groups) runs four workgroups per group of 4 tiles, each over a quarter of K, the last to
+    arrive summing the 12 slices in order: the split-K launch's bits at every M (a second call
+    checks the arrival counters were left at zero), rows of both ends of N near the oracle."""
+    import torch
+
+    from dspark_rocm import ops
+
+    n, k = 4096, 12288
+    wq, s, b = _quantized(91 + bits, n, k, bits)
+    d = _dev(wq, s, b, dev)
+    pk = ops.qmm_pack(*d, bits=bits)
+    for m in (1, 16, 33):
+        x = randn_bf16(rng(m + 5), m, k)
+        xd = to_dev_bf16(x, dev)
+        plan = ops.packed_multi_plan([xd], [pk])
+        assert plan["kernel"] == "per CU" and plan["k_parts"] == 4 and plan["tiles_per_workgroup"] == 4, plan
+        assert plan["slices"] == 12 and plan["workgroups"] == 256 * ((m + 15) // 16), plan
+        want = ops.quantized_matmul_multi([xd], [d[0]], [d[1]], [d[2]], bits=bits)[0]
+        for _ in range(2):
+            got = ops.quantized_matmul_packed_multi([xd], [pk])[0]
+            assert torch.equal(got, want), (bits, m)
+        if m == 16:
+            yh = from_dev_bf16(got)
+            for sl in (slice(0, 64), slice(n - 64, n)):
+                ref = qmm_ref.qmm_f64(x, wq[sl], s[sl], b[sl], bits)
+                assert_rms_close(yh[:, sl], ref, 2e-2, f"per-CU K parts {bits}-bit rows {sl}")
+
+
 @pytest.mark.parametrize("m", [1, 16, 33])
 def test_per_cu_kernel_two_tiles_8bit(dev, m):
     """The q/k/v launch of an 8B-shaped layer (384 tiles: two per workgroup, K in four parts)
@@ -159,7 +190,7 @@ def test_per_cu_kernel_two_tiles_8bit(dev, m):
 
     k, ns = 4096, (4096, 1024, 1024)
     x = to_dev_bf16(randn_bf16(rng(m + 77), m, k), dev)
-    for bits, kernel in ((8, "whole-K per CU"), (4, "split-K")):
+    for bits, kernel in ((8, "per CU"), (4, "split-K")):
         devs = [_dev(*_quantized(60 + i + bits, n, k, bits), dev) for i, n in enumerate(ns)]
         packs = [ops.qmm_pack(*d, bits=bits) for d in devs]
         plan = ops.packed_multi_plan([x], packs)
@@ -179,7 +210,7 @@ def test_per_cu_kernel_needs_one_x(dev):
     k, bits = 4096, 8
     packs = [ops.qmm_pack(*_dev(*_quantized(40 + i, 12288, k, bits), dev), bits=bits) for i in range(2)]
     x = to_dev_bf16(randn_bf16(rng(5), 16, k), dev)
-    assert ops.packed_multi_plan([x], packs)["kernel"] == "whole-K per CU"
+    assert ops.packed_multi_plan([x], packs)["kernel"] == "per CU"
     assert ops.packed_multi_plan([x, x.clone()], packs)["kernel"] == "split-K"
     small = ops.qmm_pack(*_dev(*_quantized(3, 1024, k, bits), dev), bits=bits)
     assert ops.packed_multi_plan([x], [small])["kernel"] == "split-K"
