@@ -47,7 +47,7 @@ struct MoeCuArgs {
 };
 
 // LDS row pitch of x (elements), the bytes of one wave's scale/bias slot (four [16][G] blocks)
-// and the workgroup's total
+// and the workgroup's total (with each wave's [G][16] table of its unit's MFMA seeds, 64 G bytes)
 template <int G>
 constexpr int moe_cu_xpitch() { return 64 * G + 8; }
 template <int G>
@@ -55,7 +55,7 @@ constexpr int moe_cu_slot() { return 4 * 32 * G; }
 template <int G, int NW>
 constexpr size_t moe_cu_lds_bytes() {
   return (size_t)kMoeCuRows * moe_cu_xpitch<G>() * 2 + (size_t)kMoeCuRows * G * 4 + 4 * kMoeCuOffsInts +
-         4 * kMoeCuMaxPairs + (size_t)NW * moe_cu_slot<G>();
+         4 * kMoeCuMaxPairs + (size_t)NW * (moe_cu_slot<G>() + 64 * G);
 }
 // loads per unit (four scale/bias blocks, then the two weight tiles) and the fewest units
 // (<= 8) whose loads fill whole windows of PF, or 0
@@ -104,6 +104,7 @@ __global__ __launch_bounds__(64 * NW) void moe_cu_kernel(const MoeCuArgs a) {
   int* const offs = reinterpret_cast<int*>(xsum + kMoeCuRows * G);         // [E + 1] bucket starts
   int* const tok = offs + kMoeCuOffsInts;                                  // token of bucket position
   char* const slots = reinterpret_cast<char*>(tok + kMoeCuMaxPairs);        // [NW][SBB]
+  float* const seeds = reinterpret_cast<float*>(slots + NW * SBB);          // [NW][G][16 rows]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int c16 = lane & 15, q = lane >> 4;
@@ -230,9 +231,16 @@ __global__ __launch_bounds__(64 * NW) void moe_cu_kernel(const MoeCuArgs a) {
       // outputs are dropped)
       auto xrow = [&](int rr) { return tok[min(cur.p0 + max(min(rr, cur.rows - 1), 0), kMoeCuMaxPairs - 1)]; };
       const u16* xl = xs + xrow(c16) * XP + k_quarter<BITS>(q);
-      const float* xsr[4];
+      // the unit's MFMA seeds (the group sums of its bucket rows) gathered once into this wave's
+      // table [G][16 rows], so each group reads its lane's 4 rows with one 16-byte read
+      float* const seed = seeds + wave * (G * 16);
+      {
+        constexpr int GL = G / 4;  // groups per lane: lane (row l % 16, groups (l / 16) * GL ..)
+        const float* src = xsum + xrow(c16) * G + q * GL;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xsr[i] = xsum + xrow(4 * q + i) * G;
+        for (int i = 0; i < GL; ++i) seed[(q * GL + i) * 16 + c16] = src[i];
+        asm volatile("" ::: "memory");
+      }
 
       f32x4_t acc[2], part[2][KW];
       u32x4_t a0[GPL], a1[GPL];  // x fragments and sums of the load's groups, read once for
@@ -263,8 +271,7 @@ __global__ __launch_bounds__(64 * NW) void moe_cu_kernel(const MoeCuArgs a) {
           if (m == 0) {
             a0[h] = lds128(xl + 64 * g);
             a1[h] = lds128(xl + 64 * g + 8);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) cs[h][i] = xsr[i][g];
+            cs[h] = *reinterpret_cast<const f32x4_t*>(&seed[g * 16 + 4 * q]);
           }
           const char* sbo = slot + 2 * m * 32 * G + c16 * 2 * G + 2 * (g & ~1);
           const u32 s2 = *reinterpret_cast<const u32*>(sbo);
