@@ -139,11 +139,13 @@ int launch_wk(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
 // tiles per workgroup split over KH K parts, on at least 180 CUs; the slices of the split-K plan
 // fix the association, so the bits are that plan's.
 //   K = 4096: TPW = ceil(tiles / 256) (2 tiles x 4 parts, or 3..6 tiles x 2 parts: 8 or 12
-//   waves) over all of K. Where measured faster than the other kernels: 3..6 tiles (C2 gate+up
-//   25.5 -> 21.3 us, 4-bit 17.9 -> 16.3), and 2 tiles at 8 bits (C2 q+k+v 9.7 -> 9.2 us; at 4
+//   waves) over all of K. Where measured faster than the other kernels: 3..6 tiles (the gate+up
+//   pair 2 x [12288, 4096] at M = 16: 25.5 -> 21.3 us, 4-bit 17.9 -> 16.3), and 2 tiles at 8
+//   bits (q+k+v, [6144, 4096]: 9.7 -> 9.2 us; at 4
 //   bits 8.3 -> 8.7, not taken). One tile per CU (x 8 K parts) measured slower than the whole-K
 //   tile kernel (7.9 -> 8.2 us) and is not taken.
-//   K = 12288 with 16-group slices, up to 256 tiles (C2 down): four workgroups per tile group,
+//   K = 12288 with 16-group slices, up to 256 tiles (the [4096, 12288] down
+//   projection): four workgroups per tile group,
 //   each over 3072 columns of K (three slices), 4 tiles x 3 waves, their partials summed by the
 //   last to arrive. (Three parts of 4096 at 3 tiles per workgroup would need 258 workgroups.)
 // Returns the shape, or tpw = 0 when the launch keeps the split-K or whole-K tile kernel.

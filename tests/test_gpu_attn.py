@@ -112,7 +112,7 @@ def test_tree_mask_every_workgroup_shape(dev, hq, hk, L, d):
 
 
 @pytest.mark.parametrize("L", [512, 4096, 16384, 32768])
-def test_c3_lengths(dev, L):
+def test_32x8x128_cache_lengths(dev, L):
     """32 q heads, 8 KV heads, D 128, 16 rows at offset L (L + 16 keys), split-KV."""
     from dspark_rocm import ops
 

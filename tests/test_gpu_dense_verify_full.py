@@ -27,7 +27,7 @@ from oracle import attn_ref, c_oracle, model_ref, moe_ref, quant_ref
 
 pytestmark = pytest.mark.gpu
 
-C5 = dict(hidden_size=5120, intermediate_size=25600, num_attention_heads=64, num_key_value_heads=8, head_dim=128,
+DENSE_5120 = dict(hidden_size=5120, intermediate_size=25600, num_attention_heads=64, num_key_value_heads=8, head_dim=128,
           vocab_size=151936, rms_norm_eps=1e-6, rope_theta=1e6, bits=8, lm_head_bits=8)
 CTX, ROWS = 16384, 16
 
@@ -39,7 +39,7 @@ def _np(t):
 def _model(dev, layers, seed):
     from dspark_rocm.model import DenseModel, ModelArgs
 
-    return DenseModel.random(ModelArgs(num_hidden_layers=layers, **C5), device=dev, seed=seed)
+    return DenseModel.random(ModelArgs(num_hidden_layers=layers, **DENSE_5120), device=dev, seed=seed)
 
 
 def _seed_prefix(caches, seed):
@@ -69,7 +69,7 @@ def _ulps_close(got, want, what, ulps=2):
     assert not bad.any(), f"{what}: {bad.sum()} elements beyond {ulps} ulps, worst {np.abs(got - want).max():.4g}"
 
 
-def test_c5_layer_and_head_full_width_against_oracle(dev):
+def test_dense_5120_layer_and_head_full_width_against_oracle(dev):
     from dspark_rocm import ops
     from dspark_rocm.model import Target
 
@@ -179,7 +179,7 @@ def test_c5_layer_and_head_full_width_against_oracle(dev):
     assert np.array_equal(_np(got[0]).argmax(-1)[clear], want.argmax(-1)[clear])
 
 
-def test_c5_64_layers_packed_is_reference_layout_and_rollback_is_exact(dev):
+def test_dense_5120_64_layers_packed_is_reference_layout_and_rollback_is_exact(dev):
     from dspark_rocm.model import Target
 
     model = _model(dev, 64, seed=61)

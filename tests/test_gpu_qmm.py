@@ -81,7 +81,7 @@ def test_more_than_16_rows(dev, bits):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_c1_full_size_against_c_oracle(dev, bits):
+def test_4096x4096_full_size_against_c_oracle(dev, bits):
     """M=16, N=K=4096 (the C restatement, fp32 factored like the kernel)."""
     x, w, s, b = _problem(0, 16, 4096, 4096, bits)
     got = _run(dev, x, w, s, b, bits)
@@ -112,7 +112,7 @@ C2_SHAPES = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288)]   # [N, K
 
 @pytest.mark.parametrize("m", [1, 4, 8, 16])
 @pytest.mark.parametrize("n,k", C2_SHAPES)
-def test_c2_layer_set_shapes_against_c_oracle(dev, n, k, m):
+def test_8b_layer_set_shapes_against_c_oracle(dev, n, k, m):
     """Every distinct [N, K] of the 8-bit layer set (q/o, k/v, gate/up, down) at each verify
     width, against the C restatement: the whole-K launch ([4096, 4096]) and the split-K plans."""
     x, w, s, b = _problem(n + k + m, m, k, n, 8, quantized=True)

@@ -116,17 +116,17 @@ def test_module_path_over_quantized_caches_matches_fused(dev, bits):
     assert (wa == wb).float().mean().item() > 0.95
 
 
-def test_c5_layer_over_8bit_kv_cache_against_oracle(dev):
+def test_dense_5120_layer_over_8bit_kv_cache_against_oracle(dev):
     """One full-width 32B-class layer (hidden 5120, 64/8 heads x 128, intermediate 25600,
     vocabulary 151936) over a 16k 8-bit quantized cache: 16 verify rows through the fused step
     against the oracle forward over the same dequantized prefix with quantized new rows."""
     from dspark_rocm.model import DenseModel, ModelArgs, Target
     from dspark_rocm.quant import quantize_rows
 
-    from test_gpu_c5_full import C5, CTX, ROWS, _Rows
+    from test_gpu_dense_verify_full import DENSE_5120, CTX, ROWS, _Rows
     from oracle import model_ref, quant_ref
 
-    model = DenseModel.random(ModelArgs(num_hidden_layers=1, **C5), device=dev, seed=71)
+    model = DenseModel.random(ModelArgs(num_hidden_layers=1, **DENSE_5120), device=dev, seed=71)
     a = model.args
     tgt = Target(model, kv_bits=8)
     cache = tgt.make_cache(CTX + 64)
@@ -151,7 +151,7 @@ def test_c5_layer_over_8bit_kv_cache_against_oracle(dev):
     ids = np.random.Generator(np.random.PCG64(73)).integers(0, a.vocab_size, ROWS)
     got, _ = tgt.verify(torch.as_tensor(ids[None]), cache)
     want = ref.forward(ids.tolist())
-    err, _ = assert_rms_close(_np(got[0]), want, 5e-2, "C5 layer + head over an 8-bit KV cache at 16k")
+    err, _ = assert_rms_close(_np(got[0]), want, 5e-2, "5120-hidden layer + head over an 8-bit KV cache at 16k")
     top2 = np.sort(want, axis=-1)[:, -2:]
     clear = (top2[:, 1] - top2[:, 0]) > 2 * err
     assert clear.sum() >= ROWS // 2
