@@ -302,10 +302,21 @@ def bench_qmm_single(dev, bits: int, m: int, n: int = 4096, k: int = 4096):
         torch.cuda.synchronize()
         singles.append(e0.elapsed_time(e1) * 1e3)
     us_single = statistics.median(singles)
+    # the same matrices in the packed qmm form (what a loaded model's projections use): same bits
+    packs = [ops.qmm_pack(*mt, bits=bits) for mt in mats]
+
+    def chain_packed():
+        for i in range(pool):
+            ops.quantized_matmul_packed(x, packs[i], out=y)
+
+    ms_packed, _ = time_graph(chain_packed)
+    us_packed = ms_packed * 1e3 / pool
+    del packs
     by = qmm_bytes(n, k, bits, m)
     return {"shape": f"{n}x{k}", "bits": bits, "M": m, "bytes": by, "us_chained": round(us_chain, 3),
             "GBs_chained": round(by / us_chain / 1e3, 1), "us_single": round(us_single, 3),
-            "GBs_single": round(by / us_single / 1e3, 1)}
+            "GBs_single": round(by / us_single / 1e3, 1), "us_chained_packed": round(us_packed, 3),
+            "GBs_chained_packed": round(by / us_packed / 1e3, 1)}
 
 
 def bench_attention(dev, L: int, hq=32, hk=8, d=128, mq=16, dtype="bf16", kv_bits: int = 16):
@@ -786,11 +797,12 @@ def main() -> None:
                 r = bench_qmm_single(dev, b, m)
                 extra["qmm_4096x4096"].append(r)
                 log(f"qmm 4096x4096 {b}-bit M={m}: {r['us_chained']} us chained ({r['GBs_chained']} GB/s), "
-                    f"{r['us_single']} us single")
+                    f"{r['us_single']} us single, packed form {r['us_chained_packed']} us chained")
                 if m == 16:
                     legs[f"qmm_4096x4096_{b}bit"] = leg(f"one 4096x4096 {b}-bit qmm, M=16, chained", r["bytes"],
                                                         r["us_chained"], mbw, 2 * 16 * 4096 * 4096,
-                                                        us_single=r["us_single"])
+                                                        us_single=r["us_single"],
+                                                        us_chained_packed=r["us_chained_packed"])
         extra["verify_attention"] = []
         for L in (512, 4096, 16384, 32768):
             r = bench_attention(dev, L)
