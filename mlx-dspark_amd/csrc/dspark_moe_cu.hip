@@ -19,12 +19,14 @@ bool offsets_fit(long E, long N, long K, int bits) {
 }
 
 // Waves per CU and loads in flight per wave (a divisor of a few units' loads, moe_cu_trip_units).
-// Measured at the 30B-A3B block (K = 2048, 4 bits, 89 live experts): 12 waves with 12 loads
-// each, 35 us per launch; 8 x 36, 16 x 12 and 12 x 18 were slower.
-constexpr int kMoeCuWaves = 12;
+// Measured at the 30B-A3B block (K = 2048, 4 bits, 89 live experts, about 17 units per CU),
+// with the per-wave seed table: 9 waves with 6 loads each, 30.9 us per launch; 6 loads per
+// wave at 8 / 10 / 11 / 12 waves 34.1 / 31.3 / 31.6 / 32.2 us, and at 12 waves 4 / 9 / 12 / 18
+// loads 33.1 / 33.5 / 34.6 / 36.0 us.
+constexpr int kMoeCuWaves = 9;
 template <int BITS, int G>
 constexpr int moe_cu_window() {
-  if (G == 32) return BITS == 4 ? 12 : 17;  // loads per unit: 36; 68
+  if (G == 32) return BITS == 4 ? 6 : 17;  // loads per unit: 36; 68
   return BITS == 4 ? 12 : 10;               // 12; 20
 }
 
