@@ -22,7 +22,8 @@ bool offsets_fit(long E, long N, long K, int bits) {
 // Measured at the 30B-A3B block (K = 2048, 4 bits, 89 live experts, about 17 units per CU),
 // with the per-wave seed table: 9 waves with 6 loads each, 30.9 us per launch; 6 loads per
 // wave at 8 / 10 / 11 / 12 waves 34.1 / 31.3 / 31.6 / 32.2 us, and at 12 waves 4 / 9 / 12 / 18
-// loads 33.1 / 33.5 / 34.6 / 36.0 us.
+// loads 33.1 / 33.5 / 34.6 / 36.0 us. At 8 bits (68 loads per unit) 17 loads: 50.5 us against
+// 54.1 / 66.2 / 69.1 us for 8 / 6 / 12.
 constexpr int kMoeCuWaves = 9;
 template <int BITS, int G>
 constexpr int moe_cu_window() {
