@@ -67,10 +67,11 @@ Plan make_plan(const long* Ns, int count, long K, long M, int bits, bool wholek_
   for (int i = 0; i < count; ++i) strips += (Ns[i] + kStripRows - 1) / kStripRows;
   p.strips = (int)strips;
   p.mtiles = (int)((M + 15) / 16);
-  // One 16-row whole-K workgroup per CU where it was measured faster than split-K: 8-bit rows,
-  // K = 4096, 240..256 tiles (a [4096, 4096] matrix, or problems adding up to it). The choice
+  // One 16-row whole-K workgroup per CU where it was measured faster than split-K: 8- or 4-bit
+  // rows, K = 4096, 240..256 tiles (a [4096, 4096] matrix, or problems adding up to it; 4-bit
+  // 8.6 -> 8.4 us at M = 16, its packed o projection in the 4-bit layer set too). The choice
   // depends on the shape only, never on M, so a row's bits do not depend on its company.
-  if (wholek_ok && bits == 8 && K == 4096) {
+  if (wholek_ok && (bits == 8 || bits == 4) && K == 4096) {
     long tiles = 0;
     for (int i = 0; i < count; ++i) tiles += (Ns[i] + 15) / 16;
     if (tiles >= 240 && tiles <= kCUs) {
@@ -129,9 +130,13 @@ int launch_bits(const QmmSkArgs& a, const Plan& p, bool sbvec, hipStream_t st) {
 constexpr int kWkWaves = 8;  // whole-K: one K octet per wave at K = 4096
 
 template <bool PACKED, bool SBVEC>
-int launch_wk(const QmmSkArgs& a, const Plan& p, hipStream_t st) {
-  hipLaunchKernelGGL((qmm_wk_kernel<8, kWkWaves, PACKED, SBVEC>), dim3(p.tiles, p.mtiles), dim3(64 * kWkWaves), 0, st,
-                     a);
+int launch_wk(const QmmSkArgs& a, const Plan& p, int bits, hipStream_t st) {
+  if (bits == 4)
+    hipLaunchKernelGGL((qmm_wk_kernel<4, kWkWaves, PACKED, SBVEC>), dim3(p.tiles, p.mtiles), dim3(64 * kWkWaves), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((qmm_wk_kernel<8, kWkWaves, PACKED, SBVEC>), dim3(p.tiles, p.mtiles), dim3(64 * kWkWaves), 0,
+                       st, a);
   return check_launch(PACKED ? "dspark_qmm_packed" : "dspark_qmm_affine");
 }
 
@@ -436,8 +441,8 @@ int multi_impl(const dspark_qmm_problem* problems, int count, int64_t M, int bit
       a.p[i].strip0 = t0;
       t0 += (int)((problems[i].N + 15) / 16);
     }
-    if (packed) return launch_wk<true, true>(a, p, s);
-    return sbvec ? launch_wk<false, true>(a, p, s) : launch_wk<false, false>(a, p, s);
+    if (packed) return launch_wk<true, true>(a, p, bits, s);
+    return sbvec ? launch_wk<false, true>(a, p, bits, s) : launch_wk<false, false>(a, p, bits, s);
   }
   if (packed) return bits == 4 ? launch_packed<4>(a, p, s) : launch_packed<8>(a, p, s);
   return bits == 4 ? launch_bits<4>(a, p, sbvec, s) : launch_bits<8>(a, p, sbvec, s);

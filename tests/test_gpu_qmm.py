@@ -190,8 +190,8 @@ def test_split_k_workspace_reuse_is_bitwise_stable(dev, bits):
     inputs = []
     for i, (n, k) in enumerate(shapes):
         x, w, s, b = _problem(50 + i, 16, k, n, bits)
-        # (the 8-bit [4096, 4096] launch takes no workspace: one whole-K workgroup per 16-row tile)
-        whole_k = bits == 8 and (n, k) == (4096, 4096)
+        # (the [4096, 4096] launch takes no workspace: one whole-K workgroup per 16-row tile)
+        whole_k = (n, k) == (4096, 4096)
         assert (_lib.load().dspark_qmm_affine_workspace(16, k, n, bits, 64) > 0) != whole_k or n * k < 2**20
         inputs.append(tuple(t(v, dev) for t, v in zip((to_dev_bf16, to_dev_packed, to_dev_bf16, to_dev_bf16),
                                                          (x, w, s, b))) + ((x, w, s, b),))

@@ -242,11 +242,13 @@ def test_skinny_plan_geometry():
         assert (p["workspace_bytes"] > 0) == (p["slices"] > 1)
         assert p | {"rows": 5} == sk.plan(5, n, k, 8)   # the plan does not depend on M (<= 16)
         assert sk.plan(33, n, k, 8)["slices"] == p["slices"]   # nor does the kernel choice, at any M
-    # the same K split serves 4 and 8 bits (the whole-K launch is 8-bit only)
+    # the same K split serves 4 and 8 bits, and so does the whole-K launch of [4096, 4096]
     assert sk.plan(16, 4096, 12288, 4)["slices"] == sk.plan(16, 4096, 12288, 8)["slices"]
-    assert sk.plan(16, 4096, 4096, 4)["slices"] == 8
+    p4 = sk.plan(16, 4096, 4096, 4)
+    assert (p4["slices"], p4["groups_per_slice"], p4["workgroups"], p4["workspace_bytes"]) == (1, 64, 256, 0)
+    assert sk.plan(16, 4096, 2048, 4)["slices"] > 1   # K = 2048 keeps split-K at both widths
     assert sk.geometry(4096, 4096) == (64, 1)
-    assert sk.geometry(4096, 4096, bits=4) == (64, 8)
+    assert sk.geometry(4096, 4096, bits=4) == (64, 1)
 
 
 def _qlinear(bits=4, out_features=64, in_features=128, bias=False):

@@ -97,7 +97,7 @@ def test_noalloc_reset_clears_stale_counters(dev):
     _lib.call("dspark_qmm_noalloc_reset", stream)
     torch.cuda.synchronize()
     assert not counters.any()
-    M, N, K, bits = 16, 4096, 4096, 4
+    M, N, K, bits = 16, 6144, 4096, 4   # a split-K plan ([4096, 4096] runs whole-K, no scratch)
     assert _workspace_bytes(lib, M, N, K, bits) > 0
     x, (w, s, b), (xd, wd, sd, bd) = _problem(rng(72), M, N, K, bits, dev)
     want = _with_workspace(lib, xd, wd, sd, bd, M, N, K, bits, stream)
